@@ -1,0 +1,217 @@
+#!/usr/bin/env python3
+"""Decode microbenchmark of the KV path on one MI355X.
+
+Workload: batch 32, 16 query / 4 KV heads, head_dim 128, bf16; per-row cache lengths drawn
+uniformly from [512, 8192] (seed 0); K/V cache, q and new k/v are N(0, 1). One step appends one
+token per row at its own position and runs single-token attention over the whole cache
+(``flash_attn_with_kvcache``), then advances the positions (``KVCache.advance``). Inputs are
+resident in HBM before timing starts; the K timed steps run as one HIP graph replay.
+
+Prints one JSON line: tokens/s (32 tokens per step), the roofline of the decode attention
+(algorithmic bytes over its event-timed duration against 8 TB/s), and the reference's CPU
+fallback timed on this host's cores on the same workload.
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+METRIC = "decode tok/s at B=32 ctx 8k GQA16/4 hd128; KV path HBM GB/s as % of peak"
+B, H, H_KV, D = 32, 16, 4, 128
+L_MIN, L_MAX = 512, 8192
+HBM_PEAK = 8.0e12
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
+    return ap.parse_args()
+
+
+def cpu_baseline(kc, vc, q, k, v, seqlens, budget_s=12.0):
+    """The reference's CPU fallback (oracle.sdpa_fallback: append + masked SDPA with GQA) on the
+    full decode workload, on this host's cores: median seconds per step over a bounded run."""
+    import torch
+    from oracle import sdpa_fallback
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    kc, vc = kc.clone(), vc.clone()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    sdpa_fallback.flash_attn_with_kvcache(q, kc, vc, k, v, seqlens, (-1, 0))  # warm-up
+    while (len(times) < 20 or time.perf_counter() < t_end) and len(times) < 400:
+        t0 = time.perf_counter()
+        sdpa_fallback.flash_attn_with_kvcache(q, kc, vc, k, v, seqlens, (-1, 0))
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), cores, len(times)
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the KV path runs per GPU "
+              f"with no cross-GPU exchange, so run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from modelcore_amd import _ext, stats
+    from modelcore_amd.cache import KVCache
+    from modelcore_amd.kernels.flash_attn import flash_attn
+
+    W, K = args.warmup, args.steps
+    dev = torch.device("cuda", 0)
+    t_alloc = L_MAX + W + K + 1  # room for every step, and for one more query position
+    log(f"generating inputs: B={B} H={H} H_kv={H_KV} D={D} T_alloc={t_alloc} steps={W}+{K}")
+    g = torch.Generator().manual_seed(args.seed)
+    seqlens = torch.randint(L_MIN, L_MAX + 1, (B,), generator=g, dtype=torch.int32)
+    kc = torch.randn(B, t_alloc, H_KV, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(B, t_alloc, H_KV, D, generator=g).to(torch.bfloat16)
+    qs = torch.randn(W + K, B, 1, H, D, generator=g).to(torch.bfloat16)
+    ks = torch.randn(W + K, B, 1, H_KV, D, generator=g).to(torch.bfloat16)
+    vs = torch.randn(W + K, B, 1, H_KV, D, generator=g).to(torch.bfloat16)
+
+    cache = KVCache(B, H_KV, t_alloc, D, 1, dev, torch.bfloat16)
+    cache.k_cache[0].copy_(kc)
+    cache.v_cache[0].copy_(vc)
+    cache.cache_seqlens.copy_(seqlens)
+    cache._pos_uniform = None  # right-ragged rows
+    qd, kd, vd = qs.to(dev), ks.to(dev), vs.to(dev)
+    k_slot, v_slot = cache.get_slot_cache(0)
+
+    def step(i):
+        y = flash_attn.flash_attn_with_kvcache(qd[i], k_slot, v_slot, k=kd[i], v=vd[i],
+                                               cache_seqlens=cache.cache_seqlens, causal=True,
+                                               window_size=(-1, 0))
+        cache.advance(1)
+        return y
+
+    log("warm-up")
+    for i in range(W):
+        y = step(i)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()
+
+    if args.eager:
+        run = lambda: [step(W + i) for i in range(K)]  # noqa: E731
+    else:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(K):
+                step(W + i)
+        run = graph.replay
+
+    log(f"timing {K} steps ({'eager' if args.eager else 'one graph replay'})")
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    run()
+    end.record()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(end) / K
+    final = cache.cache_seqlens.cpu()
+    assert torch.equal(final, seqlens + W + K), "positions did not advance once per step"
+
+    # Algorithmic bytes of the timed steps (positions grow by one per step).
+    base = seqlens.tolist()
+    step_bytes = [stats.decode_step_bytes([L + W + i for L in base], H, H_KV, D, 2)
+                  for i in range(K)]
+    mean_step_bytes = sum(step_bytes) / K
+    step_gbps = mean_step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # Dominant kernel: the decode attention (split-K pass + merge), attention only, back to back
+    # on the stream it is launched on, timed with HIP events around N launches.
+    lib = _ext.lib()
+    pos = cache.cache_seqlens  # positions now: base + W + K, each row's query at its position
+    out = torch.empty(B, 1, H, D, dtype=torch.bfloat16, device=dev)
+    ws_bytes = lib.mcamd_attn_workspace_bytes(B, 1, H, H_KV, D, t_alloc, -1)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = _ext.stream_handle(dev)
+    q_attn = qd[0]
+
+    def attn():
+        return lib.mcamd_decode_attention(q_attn.data_ptr(), k_slot.data_ptr(), v_slot.data_ptr(),
+                                          pos.data_ptr(), out.data_ptr(), B, H, H_KV, D, t_alloc,
+                                          k_slot.stride(0), -1, _ext.BF16, ws.data_ptr(), ws_bytes,
+                                          stream)
+
+    for _ in range(5):
+        _ext.check(attn(), "decode_attention")
+    n_attn = max(K, 50)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(n_attn):
+        attn()
+    end.record()
+    torch.cuda.synchronize()
+    attn_us = start.elapsed_time(end) / n_attn * 1e3
+    attn_positions = final.tolist()
+    attn_bytes = stats.decode_step_bytes(attn_positions, H, H_KV, D, 2, append=False)
+    attn_gbps = attn_bytes / (attn_us * 1e-6) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(B / (ms_per_step * 1e-3), 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode microbench: append 1 token per row + single-token attention over "
+                        "the KV cache, B=32, GQA 16q/4kv, head_dim 128, lengths U[512,8192] seed 0",
+            "batch": B, "n_head": H, "n_kv_head": H_KV, "head_dim": D,
+            "max_cache_len": t_alloc, "mean_len": round(sum(base) / B + W + K / 2, 1),
+            "timing": "eager" if args.eager else "hip_graph",
+        },
+        "kv_path_gbps": round(step_gbps, 1),
+        "kv_path_pct_peak": round(100 * step_gbps * 1e9 / HBM_PEAK, 2),
+        "roofline": {
+            "kernel": "decode_split_kernel + decode_combine_kernel (attention only)",
+            "bound": "hbm",
+            "achieved": round(attn_gbps, 1),
+            "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": round(attn_gbps * 1e9 / HBM_PEAK, 4),
+            "traffic": None,
+            "us_per_launch": round(attn_us, 2),
+            "bytes_per_launch": attn_bytes,
+        },
+    }
+
+    if not args.no_cpu_baseline:
+        log("CPU baseline: reference fallback (append + masked SDPA) on host cores")
+        med, cores, n = cpu_baseline(kc, vc, qs[0], ks[0], vs[0], seqlens)
+        result["cpu_baseline"] = {
+            "value": round(B / med, 1),
+            "unit": "tok/s",
+            "cores": cores,
+            "kind": "port",
+            "sample": f"full decode workload (B=32, lengths U[512,8192]), one step, median of {n} "
+                      f"runs; torch CPU SDPA restatement of the reference fallback",
+        }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,131 @@
+/*
+ * modelcore_amd: C ABI of the MI355X (gfx950) KV-cache and cached-attention path.
+ *
+ * Every entry point takes plain device pointers, element counts and a hipStream_t passed as
+ * `void *stream` (NULL = the null stream). Nothing here allocates device memory, synchronises
+ * the host or keeps mutable global state: work is enqueued on `stream` and the call returns.
+ * Each function returns 0 on success or a negative MCAMD_E* code; mcamd_last_error() then
+ * describes the failure (thread-local, valid until the next call on the same thread).
+ *
+ * Layouts (row-major, innermost dimension contiguous), matching the reference's cache object
+ * and FA3-style operator (modelcore/cache.py:22-23, modelcore/kernels/flash_attn.py:313-322):
+ *   k_cache, v_cache : (B, T_max, H_kv, D) per slot; `cache_batch_stride` (in elements) is the
+ *                      distance between rows b and b+1 (T_max*H_kv*D for a contiguous slot view)
+ *   q, out           : (B, T_new, H, D) contiguous
+ *   k, v (new)       : (B, T_new, H_kv, D) contiguous
+ *   cache_seqlens    : (B,) int32 on the device, the position of each row BEFORE these tokens
+ * Query t of row b sits at position p = cache_seqlens[b] + t and attends keys col with
+ * col <= p and (window < 0 or p - col <= window); softmax scale is 1/sqrt(D); query head h reads
+ * KV head h / (H / H_kv).
+ *
+ * A row whose positions fall outside [0, T_max) is not written by the append and gets NaN
+ * attention output instead of an out-of-bounds access (the reference raises an index error there;
+ * kernels cannot raise without a host sync).
+ */
+#ifndef MODELCORE_AMD_H
+#define MODELCORE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of K/V/q/out. fp16 is absent, as in the reference (modelcore/runtime.py:22-23). */
+enum { MCAMD_F32 = 0, MCAMD_BF16 = 1 };
+
+/* Status codes. */
+enum {
+  MCAMD_OK = 0,
+  MCAMD_EINVAL = -1,     /* bad argument: shape, dtype, alignment, null pointer */
+  MCAMD_EUNSUPPORTED = -2, /* valid arguments this build has no kernel for */
+  MCAMD_EWORKSPACE = -3, /* workspace missing or smaller than mcamd_attn_workspace_bytes() */
+  MCAMD_ELAUNCH = -4     /* the HIP runtime refused a launch */
+};
+
+/* Version of this ABI; bumped on any signature change. */
+int mcamd_abi_version(void);
+
+/* Description of the last failure on this thread ("" after a success). */
+const char *mcamd_last_error(void);
+
+/*
+ * KV append at per-row positions: for every row b and t < t_new,
+ *   k_cache[b, cache_seqlens[b] + t] = k[b, t]   and likewise v_cache/v,
+ * a bit-exact copy; nothing else in the caches changes.
+ * Replaces the insert step of flash_attn_with_kvcache's fallback,
+ * modelcore/kernels/flash_attn.py:336-346 (slice assignment, or index_put when ragged).
+ */
+int mcamd_kv_append(const void *k, const void *v, void *k_cache, void *v_cache,
+                    const int32_t *cache_seqlens, int64_t batch, int64_t t_new,
+                    int64_t n_kv_head, int64_t head_dim, int64_t t_max,
+                    int64_t cache_batch_stride, int dtype, void *stream);
+
+/*
+ * Replication of one cache row into many: for every slot s, destination row r in
+ * [dst_row_begin, dst_row_begin + n_rows) and position t < n_tokens,
+ *   dst[s, r, t, :, :] = src[s, 0, t, :, :]        (bit-exact, K and V)
+ * `src_k`/`src_v` point at slot 0, row 0 of the source; `row_elems` = H_kv * D; `dst_batch`
+ * is the number of rows the destination has (the copy must fit in it). Strides are in elements.
+ * Replaces KVCache.prefill's broadcast copy (modelcore/cache.py:84-85) and KVCache.prefill_row's
+ * row copy (modelcore/cache.py:106-107).
+ */
+int mcamd_kv_replicate(const void *src_k, const void *src_v, void *dst_k, void *dst_v,
+                       int64_t n_slots, int64_t src_slot_stride, int64_t dst_slot_stride,
+                       int64_t dst_batch, int64_t dst_batch_stride, int64_t dst_row_begin,
+                       int64_t n_rows, int64_t n_tokens, int64_t row_elems, int dtype,
+                       void *stream);
+
+/*
+ * Bytes of scratch the attention entry points need for these sizes (split-K partials).
+ * The caller allocates it (any 256-byte aligned device buffer) and passes it in.
+ */
+size_t mcamd_attn_workspace_bytes(int64_t batch, int64_t t_new, int64_t n_head,
+                                  int64_t n_kv_head, int64_t head_dim, int64_t t_max,
+                                  int64_t window);
+
+/*
+ * The cached-attention operator: optional append of (k, v) at cache_seqlens (k and v both
+ * NULL = no append), then attention of q over the cache under the rules at the top of this
+ * file. t_new == 1 runs split-K flash-decoding; t_new > 1 runs chunked prefill against the
+ * cache prefix. cache_seqlens is read, never advanced. `causal` is accepted for signature
+ * parity and ignored: the path is always causal.
+ * Replaces flash_attn_with_kvcache (modelcore/kernels/flash_attn.py:306-366; the FA3 call at
+ * :324-328 and the SDPA fallback at :330-366).
+ */
+int mcamd_flash_attn_with_kvcache(const void *q, const void *k, const void *v,
+                                  void *k_cache, void *v_cache, const int32_t *cache_seqlens,
+                                  void *out, int64_t batch, int64_t t_new, int64_t n_head,
+                                  int64_t n_kv_head, int64_t head_dim, int64_t t_max,
+                                  int64_t cache_batch_stride, int64_t window, int causal,
+                                  int dtype, void *workspace, size_t workspace_bytes,
+                                  void *stream);
+
+/*
+ * Attention only (no append), one query token per row: the decode half of
+ * mcamd_flash_attn_with_kvcache for t_new == 1 (modelcore/kernels/flash_attn.py:348-366 with
+ * T_new == 1). Exposed separately so the append and the attention can be timed apart.
+ */
+int mcamd_decode_attention(const void *q, const void *k_cache, const void *v_cache,
+                           const int32_t *cache_seqlens, void *out, int64_t batch,
+                           int64_t n_head, int64_t n_kv_head, int64_t head_dim, int64_t t_max,
+                           int64_t cache_batch_stride, int64_t window, int dtype,
+                           void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Attention only (no append), t_new >= 1 query tokens per row against the cache prefix: the
+ * chunked-prefill half of mcamd_flash_attn_with_kvcache (modelcore/kernels/flash_attn.py:226-244
+ * and :362-364, T_new > 1).
+ */
+int mcamd_prefill_attention(const void *q, const void *k_cache, const void *v_cache,
+                            const int32_t *cache_seqlens, void *out, int64_t batch,
+                            int64_t t_new, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
+                            int64_t t_max, int64_t cache_batch_stride, int64_t window,
+                            int dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MODELCORE_AMD_H */

@@ -1,0 +1,128 @@
+"""KVCache: drop-in for ``modelcore.cache.KVCache`` (modelcore/cache.py:13-119).
+
+Same constructor, attributes, methods and assertion messages. K and V live in two preallocated
+tensors of shape (n_slots, B, T_max, H_kv, D) in the compute dtype, zero-filled at creation
+(modelcore/cache.py:22-23): one token's K (or V) for all KV heads is a contiguous H_kv*D run,
+1 KiB at H_kv=4, D=128 in bf16, which is the unit the HIP append and decode kernels move.
+``cache_seqlens`` is the per-row position on the device (int32), and ``_pos_uniform`` its host
+mirror (the shared position, or None once rows are right-ragged).
+
+The copies of ``prefill`` and ``prefill_row`` run the HIP replication kernel
+(``mcamd_kv_replicate``); the appends happen inside the attention operator
+(``modelcore_amd.kernels.flash_attn``). Position bookkeeping (``advance``, ``reset``) stays on
+torch, as in the reference.
+"""
+from __future__ import annotations
+
+import torch
+
+from modelcore_amd import _ext
+
+
+class KVCache:
+    def __init__(self, batch_size, n_kv_head, seq_len, head_dim, num_kv_slots, device, dtype):
+        self.batch_size = batch_size
+        self.max_seq_len = seq_len
+        self.n_slots = num_kv_slots
+        self.n_kv_head = n_kv_head
+        self.head_dim = head_dim
+        # (n_slots, B, T, H, D); fewer slots than layers when layers share a KV slot.
+        self.k_cache = torch.zeros(num_kv_slots, batch_size, seq_len, n_kv_head, head_dim,
+                                   device=device, dtype=dtype)
+        self.v_cache = torch.zeros(num_kv_slots, batch_size, seq_len, n_kv_head, head_dim,
+                                   device=device, dtype=dtype)
+        # Position of each row (int32 on the device), read by the attention kernels.
+        self.cache_seqlens = torch.zeros(batch_size, dtype=torch.int32, device=device)
+        # Host mirror: the shared position of every row, or None once rows are right-ragged.
+        # Maintained without reading cache_seqlens back, so decode never syncs the host.
+        self._pos_uniform = 0
+        # Non-KV per-row state (recurrent/smear state); every tensor is (batch, ...).
+        self.state = {}
+
+    def reset(self):
+        """Back to empty. K/V are deliberately not zeroed: a row only ever reads keys at indices
+        <= its own position, all of which it wrote itself (modelcore/cache.py:38-45)."""
+        self.cache_seqlens.zero_()
+        self.state = {}
+        self._pos_uniform = 0
+
+    def get_pos(self):
+        """The single position every row is at; raises on a right-ragged cache."""
+        assert self._pos_uniform is not None, \
+            "get_pos() on a right-ragged KV cache; read cache_seqlens or check uniform_pos()"
+        return self._pos_uniform
+
+    def uniform_pos(self):
+        """get_pos() without the assert: the shared position, or None if the cache is ragged."""
+        return self._pos_uniform
+
+    def get_slot_cache(self, slot):
+        """(k_cache, v_cache) views of one KV slot, each (B, T_max, H_kv, D)."""
+        return self.k_cache[slot], self.v_cache[slot]
+
+    def advance(self, num_tokens):
+        """Advance every row by num_tokens. Keeps ragged rows' differences unchanged, which is all
+        raggedness is (modelcore/cache.py:62-73)."""
+        self.cache_seqlens += num_tokens
+        if self._pos_uniform is not None:
+            self._pos_uniform += num_tokens
+
+    def _replicate_from(self, other, row_begin, n_rows, n_tokens):
+        """HIP copy of row 0, positions [0, n_tokens), of every slot of `other` into rows
+        [row_begin, row_begin + n_rows) of this cache."""
+        _ext.require_rocm(self.k_cache, other.k_cache, what="KVCache replication")
+        if self.k_cache.dtype != other.k_cache.dtype:
+            raise TypeError(f"cache dtypes differ: {self.k_cache.dtype} vs {other.k_cache.dtype}")
+        if self.k_cache.device != other.k_cache.device:
+            raise ValueError(f"caches on different devices: {self.k_cache.device} vs "
+                             f"{other.k_cache.device}")
+        if self.n_slots == 0 or n_rows == 0 or n_tokens == 0:
+            return
+        row_elems = self.n_kv_head * self.head_dim
+        lib = _ext.lib()
+        st = lib.mcamd_kv_replicate(
+            other.k_cache.data_ptr(), other.v_cache.data_ptr(), self.k_cache.data_ptr(),
+            self.v_cache.data_ptr(), self.n_slots, other.k_cache.stride(0),
+            self.k_cache.stride(0), self.batch_size, self.k_cache.stride(1), row_begin, n_rows,
+            n_tokens, row_elems,
+            _ext.dtype_code(self.k_cache.dtype), _ext.stream_handle(self.k_cache.device))
+        _ext.check(st, "kv_replicate")
+
+    def _assert_same_geometry(self, other):
+        geometry = lambda c: (c.n_slots, c.n_kv_head, c.head_dim)
+        assert geometry(self) == geometry(other), \
+            f"cache geometry (slots, H_kv, D) differs: {geometry(self)} vs {geometry(other)}"
+
+    def prefill(self, other):
+        """Copy a batch=1 prefilled cache into every row (modelcore/cache.py:75-90): one prompt
+        prefilled once, then decoded as many samples in parallel."""
+        assert self.get_pos() == 0, "Cannot prefill a non-empty KV cache"
+        self._assert_same_geometry(other)
+        assert other.max_seq_len <= self.max_seq_len, "source cache is longer than this one"
+        other_pos = other.get_pos()
+        self._replicate_from(other, 0, self.batch_size, other_pos)
+        self.cache_seqlens.fill_(other_pos)
+        self._pos_uniform = other_pos
+        # Expand any batch=1 extra state to every row.
+        for key, value in other.state.items():
+            self.state[key] = value.expand(self.batch_size, *([-1] * (value.dim() - 1))).clone()
+
+    def prefill_row(self, row, other):
+        """Copy a batch=1 prefilled cache into row `row` only (modelcore/cache.py:92-119); rows
+        filled this way end at different positions (right-ragged)."""
+        assert other.batch_size == 1, "prefill_row copies from a batch=1 cache"
+        assert 0 <= row < self.batch_size, f"row {row} out of range for batch_size {self.batch_size}"
+        assert self.cache_seqlens[row].item() == 0, "Cannot prefill a non-empty KV cache row"
+        self._assert_same_geometry(other)
+        other_pos = other.get_pos()
+        assert other_pos <= self.max_seq_len, f"prompt of {other_pos} tokens exceeds cache length {self.max_seq_len}"
+        self._replicate_from(other, row, 1, other_pos)
+        self.cache_seqlens[row] = other_pos
+        # Per-row extra state: a zero buffer per key, shaped from the source, filled row by row.
+        for key, value in other.state.items():
+            if key not in self.state:
+                self.state[key] = value.new_zeros((self.batch_size, *value.shape[1:]))
+            self.state[key][row] = value[0]
+        # Uniform again only when every row sits at the same position (e.g. equal prompts).
+        positions = set(self.cache_seqlens.tolist())
+        self._pos_uniform = positions.pop() if len(positions) == 1 else None

@@ -1,0 +1,123 @@
+// The C ABI declared in include/modelcore_amd.h: argument checks, error reporting and the
+// orchestration of the cached-attention operator (append, then decode or chunked prefill).
+#include "kernels.h"
+
+#include <string>
+
+namespace mcamd {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string &msg) { g_last_error = msg; }
+void clear_error() { g_last_error.clear(); }
+
+int check_attn_shapes(const AttnArgs &a, bool need_workspace) {
+  if (a.dtype != MCAMD_F32 && a.dtype != MCAMD_BF16)
+    return fail(MCAMD_EINVAL, "attention: dtype must be MCAMD_F32 or MCAMD_BF16");
+  if (a.batch < 0 || a.t_new < 0 || a.n_head <= 0 || a.n_kv_head <= 0 || a.head_dim <= 0 ||
+      a.t_max <= 0)
+    return fail(MCAMD_EINVAL, "attention: sizes must be positive");
+  if (a.n_kv_head > a.n_head || a.n_head % a.n_kv_head != 0)
+    return fail(MCAMD_EINVAL, "attention: n_head must be a multiple of n_kv_head");
+  if (a.t_max > (int64_t(1) << 30) || a.batch > 65535 || a.n_head > 65535)
+    return fail(MCAMD_EUNSUPPORTED, "attention: sizes beyond the 32-bit index range of the kernels");
+  if (a.cache_batch_stride < a.t_max * a.n_kv_head * a.head_dim)
+    return fail(MCAMD_EINVAL, "attention: cache_batch_stride smaller than T_max*H_kv*D");
+  if (a.batch > 0 && (!a.q || !a.k_cache || !a.v_cache || !a.seqlens || !a.out))
+    return fail(MCAMD_EINVAL, "attention: null pointer");
+  const size_t elem = a.dtype == MCAMD_F32 ? 4 : 2;
+  if (!aligned(a.q, 16) || !aligned(a.k_cache, 16) || !aligned(a.v_cache, 16) ||
+      !aligned(a.out, 16) || (a.k_new && !aligned(a.k_new, 16)) ||
+      (a.v_new && !aligned(a.v_new, 16)) || (a.cache_batch_stride * elem) % 16 != 0)
+    return fail(MCAMD_EINVAL, "attention: tensors must be 16-byte aligned");
+  if ((a.head_dim * int64_t(elem)) % 16 != 0)
+    return fail(MCAMD_EUNSUPPORTED, "attention: head_dim * itemsize must be a multiple of 16");
+  if (need_workspace) {
+    const size_t need = decode_workspace_bytes(a.batch, a.n_head, a.head_dim, a.t_max, a.window);
+    if (!a.workspace || a.workspace_bytes < need)
+      return fail(MCAMD_EWORKSPACE, "attention: workspace smaller than mcamd_attn_workspace_bytes() (" +
+                                        std::to_string(need) + " bytes)");
+    if (!aligned(a.workspace, 16)) return fail(MCAMD_EINVAL, "attention: workspace not 16-byte aligned");
+  }
+  return MCAMD_OK;
+}
+
+}  // namespace mcamd
+
+using namespace mcamd;
+
+extern "C" int mcamd_abi_version(void) { return 1; }
+
+extern "C" const char *mcamd_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" int mcamd_kv_append(const void *k, const void *v, void *k_cache, void *v_cache,
+                               const int32_t *cache_seqlens, int64_t batch, int64_t t_new,
+                               int64_t n_kv_head, int64_t head_dim, int64_t t_max,
+                               int64_t cache_batch_stride, int dtype, void *stream) {
+  AppendArgs a{k,       v,      k_cache, v_cache, cache_seqlens,      batch, t_new,
+               n_kv_head, head_dim, t_max, cache_batch_stride, dtype, as_stream(stream)};
+  return launch_append(a);
+}
+
+extern "C" size_t mcamd_attn_workspace_bytes(int64_t batch, int64_t t_new, int64_t n_head,
+                                             int64_t n_kv_head, int64_t head_dim, int64_t t_max,
+                                             int64_t window) {
+  (void)n_kv_head;
+  if (t_new != 1 || batch <= 0) return 0;
+  return decode_workspace_bytes(batch, n_head, head_dim, t_max, window);
+}
+
+extern "C" int mcamd_decode_attention(const void *q, const void *k_cache, const void *v_cache,
+                                      const int32_t *cache_seqlens, void *out, int64_t batch,
+                                      int64_t n_head, int64_t n_kv_head, int64_t head_dim,
+                                      int64_t t_max, int64_t cache_batch_stride, int64_t window,
+                                      int dtype, void *workspace, size_t workspace_bytes,
+                                      void *stream) {
+  AttnArgs a{q,     nullptr, nullptr, k_cache, v_cache, cache_seqlens, out,
+             batch, 1,       n_head,  n_kv_head, head_dim, t_max,    cache_batch_stride,
+             window, dtype,  workspace, workspace_bytes, as_stream(stream)};
+  return launch_decode(a);
+}
+
+extern "C" int mcamd_prefill_attention(const void *q, const void *k_cache, const void *v_cache,
+                                       const int32_t *cache_seqlens, void *out, int64_t batch,
+                                       int64_t t_new, int64_t n_head, int64_t n_kv_head,
+                                       int64_t head_dim, int64_t t_max,
+                                       int64_t cache_batch_stride, int64_t window, int dtype,
+                                       void *stream) {
+  AttnArgs a{q,     nullptr, nullptr, k_cache, v_cache, cache_seqlens, out,
+             batch, t_new,   n_head,  n_kv_head, head_dim, t_max,    cache_batch_stride,
+             window, dtype,  nullptr, 0,        as_stream(stream)};
+  return launch_prefill(a);
+}
+
+extern "C" int mcamd_flash_attn_with_kvcache(const void *q, const void *k, const void *v,
+                                             void *k_cache, void *v_cache,
+                                             const int32_t *cache_seqlens, void *out,
+                                             int64_t batch, int64_t t_new, int64_t n_head,
+                                             int64_t n_kv_head, int64_t head_dim, int64_t t_max,
+                                             int64_t cache_batch_stride, int64_t window,
+                                             int causal, int dtype, void *workspace,
+                                             size_t workspace_bytes, void *stream) {
+  (void)causal;
+  if ((k == nullptr) != (v == nullptr))
+    return fail(MCAMD_EINVAL, "flash_attn_with_kvcache: pass both k and v, or neither");
+  AttnArgs a{q,     k,     v,      k_cache, v_cache,  cache_seqlens, out,
+             batch, t_new, n_head, n_kv_head, head_dim, t_max,       cache_batch_stride,
+             window, dtype, workspace, workspace_bytes, as_stream(stream)};
+  int st = check_attn_shapes(a, t_new == 1);
+  if (st != MCAMD_OK) return st;
+  if (batch == 0 || t_new == 0) {
+    clear_error();
+    return MCAMD_OK;
+  }
+  if (k) {
+    AppendArgs ap{k,       v,        k_cache, v_cache, cache_seqlens,      batch, t_new,
+                  n_kv_head, head_dim, t_max, cache_batch_stride, dtype, as_stream(stream)};
+    st = launch_append(ap);
+    if (st != MCAMD_OK) return st;
+  }
+  if (t_new == 1) return launch_decode(a);
+  a.k_new = a.v_new = nullptr;
+  return launch_prefill(a);
+}

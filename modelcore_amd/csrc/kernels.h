@@ -1,0 +1,44 @@
+// Internal launchers shared between the kernel translation units and the C ABI in capi.hip.
+// Each returns an MCAMD_* status and sets the thread-local error message on failure.
+#pragma once
+
+#include "common.h"
+
+namespace mcamd {
+
+struct AppendArgs {
+  const void *k, *v;
+  void *k_cache, *v_cache;
+  const int32_t *seqlens;
+  int64_t batch, t_new, n_kv_head, head_dim, t_max, cache_batch_stride;
+  int dtype;
+  hipStream_t stream;
+};
+int launch_append(const AppendArgs &a);
+
+struct AttnArgs {
+  const void *q;
+  const void *k_new, *v_new;  // decode only: the token at position cache_seqlens[b] is read from
+                              // here instead of the cache (NULL = read it from the cache)
+  const void *k_cache, *v_cache;
+  const int32_t *seqlens;
+  void *out;
+  int64_t batch, t_new, n_head, n_kv_head, head_dim, t_max, cache_batch_stride, window;
+  int dtype;
+  void *workspace;
+  size_t workspace_bytes;
+  hipStream_t stream;
+};
+int launch_decode(const AttnArgs &a);
+int launch_prefill(const AttnArgs &a);
+
+// Split-K geometry of the decode path: keys per split and the number of splits a row can need.
+constexpr int kDecodeSplitLen = 256;
+int64_t decode_max_splits(int64_t t_max, int64_t window);
+size_t decode_workspace_bytes(int64_t batch, int64_t n_head, int64_t head_dim, int64_t t_max,
+                              int64_t window);
+
+// Shape checks shared by every attention entry point.
+int check_attn_shapes(const AttnArgs &a, bool need_workspace);
+
+}  // namespace mcamd

@@ -1,0 +1,77 @@
+"""The reference's CPU fallback for the KV path, restated with the same torch operations
+(test infrastructure and CPU baseline; see oracle/__init__.py).
+
+* ``flash_attn_with_kvcache`` follows modelcore/kernels/flash_attn.py:330-366: one host read of
+  cache_seqlens; append by slice assignment (uniform rows) or index_put (ragged rows); keys up to
+  the furthest row; ``scaled_dot_product_attention`` with ``enable_gqa`` -- sliced and unmasked
+  for a uniform single token (:217-224), causal for a uniform full prompt (:213-215), an explicit
+  (Tq, Tk) mask for uniform chunks (:226-244), a (B, 1, T_new, Tk) mask when ragged (:246-264).
+* ``replicate`` follows KVCache.prefill's broadcast copy (modelcore/cache.py:84-85).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+
+def _uniform_attention(q, k, v, window, enable_gqa):
+    """(B, H, Tq, D) x (B, H_kv, Tk, D), every row at the same position."""
+    Tq, Tk = q.size(2), k.size(2)
+    if (window < 0 or window >= Tq) and Tq == Tk:
+        return F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=enable_gqa)
+    if Tq == 1:
+        if 0 <= window < Tk:
+            first = max(0, Tk - (window + 1))  # the last window + 1 keys
+            k, v = k[:, :, first:], v[:, :, first:]
+        return F.scaled_dot_product_attention(q, k, v, is_causal=False, enable_gqa=enable_gqa)
+    q_pos = (Tk - Tq) + torch.arange(Tq).unsqueeze(1)
+    col = torch.arange(Tk).unsqueeze(0)
+    keep = col <= q_pos
+    if 0 <= window < Tk:
+        keep &= (q_pos - col) <= window
+    return F.scaled_dot_product_attention(q, k, v, attn_mask=keep, enable_gqa=enable_gqa)
+
+
+def _ragged_mask(cache_seqlens, T_new, Tk, window):
+    q_pos = cache_seqlens.to(torch.long).unsqueeze(1) + torch.arange(T_new)  # (B, T_new)
+    col = torch.arange(Tk).view(1, 1, Tk)
+    keep = col <= q_pos.unsqueeze(2)
+    if 0 <= window < Tk:
+        keep &= (q_pos.unsqueeze(2) - col) <= window
+    return keep.unsqueeze(1)
+
+
+def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
+                            window_size=(-1, -1), force_ragged=False):
+    """CPU fallback of the operator: in-place append into k_cache/v_cache, returns (B, T_new, H, D)."""
+    B, T_new, H, D = q.shape
+    positions = cache_seqlens.tolist()
+    lo, hi = min(positions), max(positions)
+    ragged = force_ragged or lo != hi
+    if k is not None and v is not None:
+        if ragged:
+            rows = torch.arange(B).unsqueeze(1)
+            cols = cache_seqlens.to(torch.long).unsqueeze(1) + torch.arange(T_new)
+            k_cache[rows, cols] = k
+            v_cache[rows, cols] = v
+        else:
+            k_cache[:, lo:lo + T_new] = k
+            v_cache[:, lo:lo + T_new] = v
+    Tk = hi + T_new
+    qs = q.transpose(1, 2)
+    ks = k_cache[:, :Tk].transpose(1, 2)
+    vs = v_cache[:, :Tk].transpose(1, 2)
+    gqa = qs.size(1) != ks.size(1)
+    window = window_size[0]
+    if ragged:
+        keep = _ragged_mask(cache_seqlens, T_new, Tk, window)
+        y = F.scaled_dot_product_attention(qs, ks, vs, attn_mask=keep, enable_gqa=gqa)
+    else:
+        y = _uniform_attention(qs, ks, vs, window, gqa)
+    return y.transpose(1, 2)
+
+
+def replicate(dst_k, dst_v, src_k, src_v, n_tokens):
+    """Broadcast row 0 of a (S, 1, T, H_kv, D) source into every row of (S, B, T', H_kv, D)."""
+    dst_k[:, :, :n_tokens] = src_k[:, :, :n_tokens]
+    dst_v[:, :, :n_tokens] = src_v[:, :, :n_tokens]

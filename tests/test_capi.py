@@ -1,0 +1,76 @@
+"""The C-ABI library on the CPU host: it loads, exports exactly what include/modelcore_amd.h
+declares, and rejects bad arguments before touching the GPU (no kernel runs here)."""
+import ctypes
+import re
+
+import pytest
+
+from conftest import ROOT
+from modelcore_amd import _ext
+
+HEADER = ROOT / "include" / "modelcore_amd.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(mcamd_\w+)\s*\(", text))
+
+
+def test_header_and_loader_agree_on_the_exported_functions():
+    assert declared_functions() == set(_ext.SIGNATURES)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _ext.lib()
+    raw = ctypes.CDLL(str(_ext.LIB_PATH))
+    for name in declared_functions():
+        assert hasattr(raw, name), name
+    assert lib.mcamd_abi_version() == _ext.ABI_VERSION
+
+
+def test_bad_dtype_and_null_pointers_are_rejected_with_a_message():
+    lib = _ext.lib()
+    st = lib.mcamd_kv_append(None, None, None, None, None, 1, 1, 1, 8, 4, 32, 7, None)
+    assert st == _ext.EINVAL and b"dtype" in lib.mcamd_last_error()
+    st = lib.mcamd_kv_append(None, None, None, None, None, 1, 1, 1, 8, 4, 32, _ext.BF16, None)
+    assert st == _ext.EINVAL and b"null" in lib.mcamd_last_error()
+
+
+def test_attention_rejects_bad_head_grouping_and_small_workspace():
+    lib = _ext.lib()
+    fake = 1 << 20  # never dereferenced: the checks fail first
+    st = lib.mcamd_decode_attention(fake, fake, fake, fake, fake, 2, 6, 4, 128, 64, 64 * 4 * 128,
+                                    -1, _ext.BF16, fake, 1 << 30, None)
+    assert st == _ext.EINVAL and b"multiple" in lib.mcamd_last_error()
+    st = lib.mcamd_decode_attention(fake, fake, fake, fake, fake, 2, 8, 4, 128, 64, 64 * 4 * 128,
+                                    -1, _ext.BF16, fake, 16, None)
+    assert st == _ext.EWORKSPACE and b"workspace" in lib.mcamd_last_error()
+    st = lib.mcamd_flash_attn_with_kvcache(fake, fake, None, fake, fake, fake, fake, 2, 1, 8, 4,
+                                           128, 64, 64 * 4 * 128, -1, 1, _ext.BF16, fake, 1 << 30,
+                                           None)
+    assert st == _ext.EINVAL and b"both k and v" in lib.mcamd_last_error()
+
+
+def test_workspace_size_follows_the_split_count():
+    lib = _ext.lib()
+    B, H, D, T_max = 32, 16, 128, 8300
+    n_splits = -(-T_max // 256)
+    want = B * H * n_splits * (D + 2) * 4
+    got = lib.mcamd_attn_workspace_bytes(B, 1, H, 4, D, T_max, -1)
+    assert want <= got < want + 256
+    windowed = lib.mcamd_attn_workspace_bytes(B, 1, H, 4, D, T_max, 1024)
+    assert windowed < got
+    assert lib.mcamd_attn_workspace_bytes(B, 7, H, 4, D, T_max, -1) == 0  # prefill needs none
+
+
+def test_a_missing_library_raises_with_its_reason(monkeypatch, tmp_path):
+    monkeypatch.setattr(_ext, "LIB_PATH", tmp_path / "absent.so")
+    _ext.reload()
+    try:
+        with pytest.raises(RuntimeError, match="not found"):
+            _ext.lib()
+        assert "absent.so" in _ext.LOAD_ERROR
+    finally:
+        monkeypatch.undo()
+        _ext.reload()
+    _ext.lib()

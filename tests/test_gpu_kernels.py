@@ -1,0 +1,326 @@
+"""Parity of the HIP kernels with the CPU oracle, through the C ABI and the drop-in operator.
+
+Append and replication must be bit-exact; attention must be within the tolerance of its dtype
+(max-abs 2e-2 for bf16 inputs with fp32 accumulation, 2e-5 for fp32) of the float64 oracle.
+Inputs are drawn on the CPU from a seeded generator and copied to the GPU, so both sides see
+identical bytes.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from _util import ATOL, bits, gen, make_case, max_abs, to_np
+from modelcore_amd import _ext
+from modelcore_amd.cache import KVCache
+from modelcore_amd.kernels.flash_attn import flash_attn
+from oracle import kv_oracle as ko
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+
+
+def _gpu(c):
+    return {k: v.to(DEV) for k, v in c.items()}
+
+
+def _note(*a):
+    print("case:", *a, flush=True)
+
+
+def test_the_hip_library_loads_on_the_gpu_box_with_one_hip_runtime():
+    assert torch.cuda.is_available(), "no ROCm GPU visible"
+    _ext.lib()
+    torch.zeros(1, device=DEV)
+    with open("/proc/self/maps") as f:
+        hip = {line.split()[-1] for line in f if "libamdhip64" in line}
+    assert len(hip) == 1, f"more than one HIP runtime mapped: {hip}"
+    with open("/proc/self/maps") as f:
+        assert any(str(_ext.LIB_PATH) in line for line in f)
+
+
+# --- append -------------------------------------------------------------------------------------
+
+APPEND_CASES = [
+    # seqlens, T_new, H_kv, D, T_max
+    ([0, 5, 11, 3], 1, 4, 128, 16),
+    ([7, 7], 5, 8, 128, 32),
+    ([0, 100, 37], 64, 2, 64, 200),
+    ([2, 9], 3, 2, 16, 16),
+    ([1, 0, 4], 2, 1, 16, 8),  # 32-byte rows of bf16: the 16-byte path; fp32 too
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("seqlens,T_new,H_kv,D,T_max", APPEND_CASES)
+def test_append_is_bit_exact(dtype, seqlens, T_new, H_kv, D, T_max):
+    _note("append", dtype, seqlens, T_new, H_kv, D, T_max)
+    c = make_case(seqlens, T_new, H_kv, H_kv, D, T_max, dtype, seed=11)
+    g = _gpu(c)
+    lib = _ext.lib()
+    st = lib.mcamd_kv_append(g["k"].data_ptr(), g["v"].data_ptr(), g["k_cache"].data_ptr(),
+                             g["v_cache"].data_ptr(), g["cache_seqlens"].data_ptr(), len(seqlens),
+                             T_new, H_kv, D, T_max, g["k_cache"].stride(0), _ext.dtype_code(dtype),
+                             _ext.stream_handle(DEV))
+    _ext.check(st, "append")
+    ek, ev = ko.append(bits(c["k_cache"]), bits(c["v_cache"]), bits(c["k"]), bits(c["v"]), seqlens)
+    assert np.array_equal(bits(g["k_cache"]), ek)
+    assert np.array_equal(bits(g["v_cache"]), ev)
+
+
+def test_append_leaves_rows_past_the_cache_untouched():
+    c = make_case([3, 15], 2, 2, 2, 64, 16, torch.bfloat16, seed=12)
+    g = _gpu(c)
+    lib = _ext.lib()
+    _ext.check(lib.mcamd_kv_append(g["k"].data_ptr(), g["v"].data_ptr(), g["k_cache"].data_ptr(),
+                                   g["v_cache"].data_ptr(), g["cache_seqlens"].data_ptr(), 2, 2, 2,
+                                   64, 16, g["k_cache"].stride(0), _ext.BF16,
+                                   _ext.stream_handle(DEV)), "append")
+    got = bits(g["k_cache"])
+    assert np.array_equal(got[1, :15], bits(c["k_cache"])[1, :15])
+    assert np.array_equal(got[1, 15], bits(c["k"])[1, 0])  # position 15 fits, 16 does not
+    assert np.array_equal(got[0, 3:5], bits(c["k"])[0])
+
+
+# --- replication --------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("slots,rows,P,H_kv,D", [(2, 4, 7, 2, 8), (3, 64, 129, 8, 128),
+                                                 (1, 5, 33, 1, 16)])
+def test_prefill_replicates_bit_exactly(dtype, slots, rows, P, H_kv, D):
+    _note("replicate", dtype, slots, rows, P, H_kv, D)
+    g = gen(13)
+    src = KVCache(1, H_kv, P, D, slots, DEV, dtype)
+    src.k_cache.copy_(torch.randn(src.k_cache.shape, generator=g).to(dtype))
+    src.v_cache.copy_(torch.randn(src.v_cache.shape, generator=g).to(dtype))
+    src.advance(P)
+    dst = KVCache(rows, H_kv, P + 5, D, slots, DEV, dtype)
+    dst.prefill(src)
+    assert dst.get_pos() == P and dst.cache_seqlens.tolist() == [P] * rows
+    ek, ev = ko.replicate(bits(dst.k_cache) * 0, bits(dst.v_cache) * 0, bits(src.k_cache),
+                          bits(src.v_cache), P, range(rows))
+    assert np.array_equal(bits(dst.k_cache), ek) and np.array_equal(bits(dst.v_cache), ev)
+
+
+def test_prefill_row_copies_only_its_row_and_tracks_raggedness():
+    g = gen(14)
+
+    def filled(n):
+        c = KVCache(1, 2, n, 8, 2, DEV, torch.float32)
+        c.k_cache.copy_(torch.randn(c.k_cache.shape, generator=g))
+        c.v_cache.copy_(torch.randn(c.v_cache.shape, generator=g))
+        c.advance(n)
+        return c
+
+    a, b = filled(5), filled(11)
+    dst = KVCache(3, 2, 24, 8, 2, DEV, torch.float32)
+    dst.prefill_row(1, a)
+    assert dst.cache_seqlens.tolist() == [0, 5, 0]
+    assert torch.equal(dst.k_cache[:, 1, :5], a.k_cache[:, 0, :5])
+    assert dst.k_cache[:, 0].abs().sum() == 0 and dst.k_cache[:, 2].abs().sum() == 0
+    dst.prefill_row(2, b)
+    assert dst.cache_seqlens.tolist() == [0, 5, 11] and dst.uniform_pos() is None
+    assert torch.equal(dst.v_cache[:, 2, :11], b.v_cache[:, 0, :11])
+    assert not dst.v_cache[:, 2, 11:].any()
+
+
+# --- attention ----------------------------------------------------------------------------------
+
+def _run_op(c, window, with_append=True):
+    g = _gpu(c)
+    out = flash_attn.flash_attn_with_kvcache(
+        g["q"], g["k_cache"], g["v_cache"], k=g["k"] if with_append else None,
+        v=g["v"] if with_append else None, cache_seqlens=g["cache_seqlens"], causal=True,
+        window_size=(window, 0))
+    torch.cuda.synchronize()
+    return out, g
+
+
+def _oracle(c, window, with_append=True):
+    q, kc, vc = to_np(c["q"]), to_np(c["k_cache"]), to_np(c["v_cache"])
+    k = to_np(c["k"]) if with_append else None
+    v = to_np(c["v"]) if with_append else None
+    return ko.flash_attn_with_kvcache(q, kc, vc, k, v, c["cache_seqlens"].tolist(), window)[0]
+
+
+DECODE_CASES = [
+    # seqlens, H, H_kv, D, T_max, window
+    ([37, 300, 0, 511], 16, 4, 128, 520, -1),
+    ([37, 300, 0, 511], 16, 4, 128, 520, 64),
+    ([1000, 1023, 5], 12, 4, 128, 1030, 100),
+    ([77, 250], 32, 8, 128, 300, -1),
+    ([255, 256, 257, 513], 8, 8, 64, 520, -1),
+    ([9, 30], 2, 2, 16, 40, 8),
+    ([60, 3], 16, 2, 64, 64, -1),   # G = 8
+    ([60, 3], 16, 1, 64, 64, 0),    # G = 16: two head chunks; window 0
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("seqlens,H,H_kv,D,T_max,window", DECODE_CASES)
+def test_decode_matches_the_oracle(dtype, seqlens, H, H_kv, D, T_max, window):
+    _note("decode", dtype, seqlens, H, H_kv, D, T_max, window)
+    c = make_case(seqlens, 1, H, H_kv, D, T_max, dtype, seed=21)
+    out, g = _run_op(c, window)
+    ref = _oracle(c, window)
+    err = max_abs(to_np(out), ref)
+    assert err <= ATOL[dtype], f"max-abs {err}"
+    ek, _ = ko.append(bits(c["k_cache"]), bits(c["v_cache"]), bits(c["k"]), bits(c["v"]), seqlens)
+    assert np.array_equal(bits(g["k_cache"]), ek)
+
+
+def test_decode_without_append_reads_the_cache():
+    seqlens = [40, 7]
+    c = make_case(seqlens, 1, 8, 2, 128, 64, torch.bfloat16, seed=22)
+    out, g = _run_op(c, -1, with_append=False)
+    assert max_abs(to_np(out), _oracle(c, -1, with_append=False)) <= ATOL[torch.bfloat16]
+    assert torch.equal(g["k_cache"].cpu(), c["k_cache"])
+
+
+PREFILL_CASES = [
+    # seqlens, T_new, H, H_kv, D, T_max, window
+    ([0, 0], 40, 8, 2, 128, 64, -1),
+    ([0, 0], 40, 8, 2, 128, 64, 9),
+    ([17, 3], 25, 16, 4, 128, 64, -1),
+    ([100, 0, 31], 70, 12, 4, 64, 200, 50),
+    ([5, 9], 3, 2, 2, 16, 16, -1),
+    ([0], 12, 2, 2, 16, 12, 8),
+    ([33, 2], 130, 32, 8, 128, 200, 0),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("seqlens,T_new,H,H_kv,D,T_max,window", PREFILL_CASES)
+def test_chunked_prefill_matches_the_oracle(dtype, seqlens, T_new, H, H_kv, D, T_max, window):
+    _note("prefill", dtype, seqlens, T_new, H, H_kv, D, T_max, window)
+    c = make_case(seqlens, T_new, H, H_kv, D, T_max, dtype, seed=31)
+    out, g = _run_op(c, window)
+    err = max_abs(to_np(out), _oracle(c, window))
+    assert err <= ATOL[dtype], f"max-abs {err}"
+    ek, ev = ko.append(bits(c["k_cache"]), bits(c["v_cache"]), bits(c["k"]), bits(c["v"]), seqlens)
+    assert np.array_equal(bits(g["k_cache"]), ek) and np.array_equal(bits(g["v_cache"]), ev)
+
+
+def test_no_cache_attention_equals_prefill_from_empty():
+    c = make_case([0, 0], 48, 8, 2, 128, 48, torch.bfloat16, seed=32)
+    g = _gpu(c)
+    y = flash_attn.flash_attn_func(g["q"], g["k_cache"], g["v_cache"], causal=True,
+                                   window_size=(16, 0))
+    ref = ko.attention(to_np(c["q"]), to_np(c["k_cache"]), to_np(c["v_cache"]), [0, 0], 16)
+    assert max_abs(to_np(y), ref) <= ATOL[torch.bfloat16]
+
+
+# --- the decode microbenchmark's own shape, at full size -----------------------------------------
+
+def test_decode_at_batch_32_gqa_16_4_hd128_context_8k():
+    """B=32, H=16, H_kv=4, D=128, cache 8192+8, lengths U[512, 8192] (seed 0): one step."""
+    g = gen(0)
+    B, H, H_kv, D, T_max = 32, 16, 4, 128, 8192 + 8
+    seqlens = torch.randint(512, 8192 + 1, (B,), generator=g, dtype=torch.int32)
+    kc = torch.randn(B, T_max, H_kv, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(B, T_max, H_kv, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, 1, H, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, 1, H_kv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, 1, H_kv, D, generator=g).to(torch.bfloat16)
+    c = dict(q=q, k=k, v=v, k_cache=kc, v_cache=vc, cache_seqlens=seqlens)
+    out, gg = _run_op(c, -1)
+    out = to_np(out)
+    kcn, vcn = to_np(kc), to_np(vc)
+    worst = 0.0
+    for b in range(B):
+        L = int(seqlens[b])
+        kb, vb = kcn[b:b + 1, :L + 1].copy(), vcn[b:b + 1, :L + 1].copy()
+        kb[0, L], vb[0, L] = to_np(k)[b, 0], to_np(v)[b, 0]
+        ref = ko.attention(to_np(q)[b:b + 1], kb, vb, [L], -1)
+        worst = max(worst, max_abs(out[b:b + 1], ref))
+    assert worst <= ATOL[torch.bfloat16], f"max-abs {worst}"
+    got = gg["k_cache"]
+    for b in range(B):
+        assert torch.equal(got[b, int(seqlens[b])].cpu(), k[b, 0])
+
+
+# --- the reference's operator invariants (modelcore/tests/test_kernels.py:420-545) on the GPU ---
+
+class TestRaggedOperator:
+    H, D, T_MAX = 4, 16, 48
+
+    def _make(self, seqlens, T_new=1, seed=0):
+        return make_case(seqlens, T_new, self.H, self.H, self.D, self.T_MAX, torch.bfloat16, seed,
+                         fill_stale=False)
+
+    @pytest.mark.parametrize("window", [-1, 8])
+    @pytest.mark.parametrize("T_new", [1, 3])
+    def test_batched_ragged_matches_each_row_alone(self, window, T_new):
+        seqlens = [4, 17, 31, 9]
+        c = self._make(seqlens, T_new)
+        out, _ = _run_op(c, window)
+        for b in range(len(seqlens)):
+            row = {k: v[b:b + 1] for k, v in c.items()}
+            o, _ = _run_op(row, window)
+            assert torch.equal(out[b:b + 1], o)
+
+    def test_stale_kv_beyond_a_rows_content_is_unreachable(self):
+        seqlens = [4, 17, 31, 9]
+        c = self._make(seqlens)
+        clean, _ = _run_op(c, -1)
+        dirty = dict(c)
+        dirty["k_cache"], dirty["v_cache"] = c["k_cache"].clone(), c["v_cache"].clone()
+        for b, L in enumerate(seqlens):
+            dirty["k_cache"][b, L + 1:] = 1e4
+            dirty["v_cache"][b, L + 1:] = float("nan")
+        assert torch.equal(clean, _run_op(dirty, -1)[0])
+
+    def test_new_tokens_land_at_each_rows_own_offset(self):
+        seqlens = [4, 17, 31, 9]
+        c = self._make(seqlens)
+        _, g = _run_op(c, -1)
+        kc = g["k_cache"].cpu()
+        for b, L in enumerate(seqlens):
+            assert torch.equal(kc[b, L], c["k"][b, 0])
+            keep = torch.ones(self.T_MAX, dtype=torch.bool)
+            keep[L] = False
+            assert torch.equal(kc[b][keep], c["k_cache"][b][keep])
+
+    def test_sliding_window_is_measured_from_each_rows_own_position(self):
+        window = 8
+        c = self._make([3, 20])
+        base, _ = _run_op(c, window)
+        far = dict(c, k_cache=c["k_cache"].clone())
+        far["k_cache"][1, :10] += 5.0
+        assert torch.equal(base[1], _run_op(far, window)[0][1])
+        near = dict(c, k_cache=c["k_cache"].clone())
+        near["k_cache"][0, 0] += 5.0
+        assert not torch.equal(base[0], _run_op(near, window)[0][0])
+
+    def test_uniform_positions_agree_with_the_oracle_and_the_ragged_rows(self):
+        for window in (-1, 8):
+            c = self._make([13, 13])
+            out, _ = _run_op(c, window)
+            assert max_abs(to_np(out), _oracle(c, window)) <= ATOL[torch.bfloat16]
+            alone, _ = _run_op({k: v[1:] for k, v in c.items()}, window)
+            assert torch.equal(out[1:], alone)
+
+
+def test_prefill_then_decode_through_the_cache_object():
+    """TestSDPAOnly.test_kvcache (modelcore/tests/test_kernels.py:372-414), checked against the
+    oracle at each call: a 16-token prefill then single tokens, positions advancing."""
+    B, T_max, H, D = 2, 64, 4, 32
+    cache = KVCache(batch_size=B, n_kv_head=H, seq_len=T_max, head_dim=D, num_kv_slots=1,
+                    device=DEV, dtype=torch.bfloat16)
+    kc, vc = cache.get_slot_cache(0)
+    g = gen(40)
+    ref_k, ref_v = np.zeros((B, T_max, H, D)), np.zeros((B, T_max, H, D))
+    for T_new in (16, 1, 1, 1):
+        q, k, v = (torch.randn(B, T_new, H, D, generator=g).to(torch.bfloat16) for _ in range(3))
+        pos = cache.get_pos()
+        y = flash_attn.flash_attn_with_kvcache(q.to(DEV), kc, vc, k=k.to(DEV), v=v.to(DEV),
+                                               cache_seqlens=cache.cache_seqlens, causal=True,
+                                               window_size=(T_max, 0))
+        cache.advance(T_new)
+        assert y.shape == (B, T_new, H, D) and cache.get_pos() == pos + T_new
+        want, ref_k, ref_v = ko.flash_attn_with_kvcache(to_np(q), ref_k, ref_v, to_np(k), to_np(v),
+                                                        [pos] * B, T_max)
+        assert max_abs(to_np(y), want) <= ATOL[torch.bfloat16]
+    assert np.array_equal(to_np(kc), ref_k)
