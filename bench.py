@@ -140,7 +140,7 @@ def main():
     pos = cache.cache_seqlens  # positions now: base + W + K, each row's query at its position
     out = torch.empty(B, 1, H, D, dtype=torch.bfloat16, device=dev)
     ws_bytes = lib.mcamd_attn_workspace_bytes(B, 1, H, H_KV, D, t_alloc, -1)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # merge counters start at zero
     stream = _ext.stream_handle(dev)
     q_attn = qd[0]
 

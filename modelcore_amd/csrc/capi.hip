@@ -33,7 +33,8 @@ int check_attn_shapes(const AttnArgs &a, bool need_workspace) {
   if ((a.head_dim * int64_t(elem)) % 16 != 0)
     return fail(MCAMD_EUNSUPPORTED, "attention: head_dim * itemsize must be a multiple of 16");
   if (need_workspace) {
-    const size_t need = decode_workspace_bytes(a.batch, a.n_head, a.head_dim, a.t_max, a.window);
+    const size_t need =
+        decode_workspace_bytes(a.batch, a.n_head, a.n_kv_head, a.head_dim, a.t_max, a.window);
     if (!a.workspace || a.workspace_bytes < need)
       return fail(MCAMD_EWORKSPACE, "attention: workspace smaller than mcamd_attn_workspace_bytes() (" +
                                         std::to_string(need) + " bytes)");
@@ -62,9 +63,8 @@ extern "C" int mcamd_kv_append(const void *k, const void *v, void *k_cache, void
 extern "C" size_t mcamd_attn_workspace_bytes(int64_t batch, int64_t t_new, int64_t n_head,
                                              int64_t n_kv_head, int64_t head_dim, int64_t t_max,
                                              int64_t window) {
-  (void)n_kv_head;
-  if (t_new != 1 || batch <= 0) return 0;
-  return decode_workspace_bytes(batch, n_head, head_dim, t_max, window);
+  if (t_new != 1 || batch <= 0 || n_kv_head <= 0 || n_head < n_kv_head) return 0;
+  return decode_workspace_bytes(batch, n_head, n_kv_head, head_dim, t_max, window);
 }
 
 extern "C" int mcamd_decode_attention(const void *q, const void *k_cache, const void *v_cache,
@@ -111,13 +111,13 @@ extern "C" int mcamd_flash_attn_with_kvcache(const void *q, const void *k, const
     clear_error();
     return MCAMD_OK;
   }
+  if (t_new == 1) return launch_decode(a);  // appends k/v itself
   if (k) {
     AppendArgs ap{k,       v,        k_cache, v_cache, cache_seqlens,      batch, t_new,
                   n_kv_head, head_dim, t_max, cache_batch_stride, dtype, as_stream(stream)};
     st = launch_append(ap);
     if (st != MCAMD_OK) return st;
   }
-  if (t_new == 1) return launch_decode(a);
   a.k_new = a.v_new = nullptr;
   return launch_prefill(a);
 }

@@ -1,0 +1,576 @@
+// Single-token decode for bf16 caches with head_dim 128: append + attention in one balanced
+// streaming pass over the cache, then a small merge pass.
+//
+// Semantics: modelcore/kernels/flash_attn.py:336-366 with T_new == 1 -- the new token's K/V land
+// at p = cache_seqlens[b], and the query of row b attends keys [lo, p], lo = max(0, p - window)
+// (window < 0: lo = 0); query head h reads KV head h / G; scale 1/sqrt(128).
+//
+// Layout facts the design rests on: the cache is (B, T_max, H_kv, 128) bf16, so one token's
+// K (or V) for four consecutive KV heads is one contiguous 1 KiB run -- a whole wave64 load of
+// 16 bytes per lane. On MI355X, streaming reads in such runs, with every CU given the same number
+// of bytes, sustain ~6.5 TB/s; reads of one head's 256 bytes at a 1 KiB stride, or uneven work
+// per CU, fall well short of that.
+//
+// Work split. A unit is (row b, group of four KV heads, group of up to four query heads per KV
+// head). Laid end to end, the units' keys form T = sum_b n_b * units slots (n_b = p_b - lo_b + 1).
+// The grid has a fixed number W of waves (one per SIMD), and wave w takes the slots
+// [w*T/W, (w+1)*T/W): equal bytes for every SIMD whatever the row lengths. A wave's range is one
+// or a few contiguous segments of units. Every wave derives T and its first row from
+// cache_seqlens itself (a scan over the rows), so nothing is synchronised with the host.
+//
+// Inside a segment, lane (r, c) = (lane / 16, lane % 16) owns KV head 4*group + r and the 16
+// bytes of dims c*8..c*8+7; a tile is four tokens (four loads each for K and V, the next tile's
+// loads in flight while the current one is consumed).
+//  * Scores: each lane forms partial dot products of its 8 dims with its KV head's 4 query heads
+//    (v_dot2_f32_bf16 on packed bf16 pairs: 16 partials, 4 tokens x 4 heads), then a four-step
+//    reduce-scatter over the 16 lanes of its row (DPP row_mirror, row_half_mirror, quad_perm)
+//    leaves lane c with the complete score of token c/4 for head c%4.
+//  * Softmax: a running maximum per head; a new maximum forces the rescale of the accumulators
+//    only when it exceeds the current one by more than 2^8 (exp2 domain), so weights stay <= 256.
+//  * Values: the 16 weights of a tile are broadcast inside the row (DPP row_newbcast) and packed
+//    to bf16 pairs of consecutive tokens; the V rows of the same two tokens are interleaved with
+//    v_perm_b32, so each v_dot2_f32_bf16 adds two tokens' contributions to one output dim.
+//  * Output: a segment that covers its whole unit writes the normalised output; otherwise it
+//    writes (o, m, l) for its 16 heads to workspace slot wave + unit (distinct per segment, since
+//    units advance with the waves), and the merge pass combines a unit's segments by
+//    log-sum-exp.
+//  * Append: the segment that ends at p reads the new token from k/v instead of the cache and
+//    its lanes store it into the cache at p (bit-exact copy; the first query-head group only).
+#include "kernels.h"
+
+#include <cmath>
+
+namespace mcamd {
+namespace {
+
+constexpr int D = 128;
+constexpr int GM = 4;                 // query heads per KV head in one unit
+constexpr int KG = 4;                 // KV heads per unit (one per row of 16 lanes)
+constexpr int kTokens = 4;            // tokens per tile
+constexpr float kRescaleSlack = 8.f;  // log2 units
+constexpr int kMaxGroups = 1024;      // 4-wave workgroups per launch, at most
+constexpr int kGroupsPerCU = 1;       // one wave per SIMD
+constexpr int kMinKeysPerGroup = 256; // fewer workgroups when the whole job is small
+constexpr int kPart = KG * GM * D + 2 * KG * GM;  // floats per partial: o[16][D], (m, l)[16]
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+struct FusedParams {
+  const uint16_t *q, *k_new, *v_new;
+  uint16_t *k_cache, *v_cache;
+  const int32_t *seqlens;
+  uint16_t *out;
+  float *part;    // [n_groups + B * n_units][kPart]: segment partials, slot = group + unit
+  int *counters;  // [B * n_units]: partials of the unit published so far (zero between calls)
+  int B, H, H_kv, G, n_hc, n_kg, n_units, T_max, window, n_groups;
+  int64_t cache_b;
+  float scale_log2;
+};
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                         __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+// DPP controls (GFX9 encoding).
+constexpr int kRowMirror = 0x140;
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kQuadSwap3 = 0x1B;  // quad_perm [3,2,1,0]
+constexpr int kQuadSwap1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kRowRor4 = 0x124;
+constexpr int kRowRor8 = 0x128;
+constexpr int kRowNewBcast = 0x150;  // + lane within the row
+constexpr int kQuadBcast[4] = {0x00, 0x55, 0xAA, 0xFF};
+
+template <int H>
+__device__ __forceinline__ float quad_bcast(float x) {
+  return dpp<kQuadBcast[H]>(x);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+__device__ __forceinline__ float exp2_or_zero(float x) {
+  // exp2 of a difference whose left side may be -inf (masked key, or no key yet).
+  return x == -INFINITY || x != x ? 0.f : fast_exp2(x);
+}
+
+// One reduce-scatter step over pairs of lanes (partner chosen by CTRL): a lane keeps the upper
+// or lower half of v[0, 2N) according to `up`, adds the partner's copy of that half, and leaves
+// the result in v[0, N).
+template <int N, int CTRL>
+__device__ __forceinline__ void rs_step(float (&v)[16], bool up) {
+#pragma unroll
+  for (int m = 0; m < N; ++m) {
+    const float keep = up ? v[m + N] : v[m];
+    const float send = up ? v[m] : v[m + N];
+    v[m] = keep + dpp<CTRL>(send);
+  }
+}
+
+struct Tile {
+  uint4 k[kTokens], v[kTokens];
+};
+
+// Keys of row b (the range [lo, pos]), or 0 for a row whose position is outside the cache.
+__device__ __forceinline__ int row_keys(const FusedParams &P, int b, int &lo) {
+  const int pos = P.seqlens[b];
+  if (pos < 0 || pos >= P.T_max) {
+    lo = 0;
+    return 0;
+  }
+  lo = key_lo(pos, P.window);
+  return pos - lo + 1;
+}
+
+// Workgroup owning flattened slot x when T slots are shared out as [g*T/NG, (g+1)*T/NG).
+__device__ __forceinline__ int group_of(int64_t x, int64_t T, int NG) {
+  return int(((x + 1) * NG + T - 1) / T - 1);
+}
+
+// Agent-scope (coherent across XCDs) relaxed accesses for the cross-workgroup partials.
+__device__ __forceinline__ void store_agent2(float *p, float a, float b) {
+  const uint64_t v = (uint64_t(__float_as_uint(b)) << 32) | __float_as_uint(a);
+  __hip_atomic_store(reinterpret_cast<uint64_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_agent2(float *p) {
+  const uint64_t v =
+      __hip_atomic_load(reinterpret_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float(uint32_t(v)), __uint_as_float(uint32_t(v >> 32)));
+}
+// s_waitcnt vmcnt(0): every store of this wave has been acknowledged.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+__device__ __forceinline__ int64_t shfl_i64(int64_t v, int src) {
+  const int lo = __shfl(int(uint64_t(v)), src, 64);
+  const int hi = __shfl(int(uint64_t(v) >> 32), src, 64);
+  return int64_t((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
+}
+
+__device__ __forceinline__ int64_t scan_incl_i64(int64_t v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int64_t u = shfl_i64(v, max(lane - off, 0));
+    if (lane >= off) v += u;
+  }
+  return v;
+}
+
+// Slots of rows [0, b_end) (every lane gets it).
+__device__ int64_t slots_before(const FusedParams &P, int b_end, int lane) {
+  int64_t total = 0;
+  for (int b0 = 0; b0 < b_end; b0 += 64) {
+    int lo;
+    const int nk = b0 + lane < b_end ? row_keys(P, b0 + lane, lo) : 0;
+    total += shfl_i64(scan_incl_i64(int64_t(nk) * P.n_units, lane), 63);
+  }
+  return total;
+}
+
+// Row holding slot x, and the first slot of that row.
+__device__ void find_row(const FusedParams &P, int64_t x, int lane, int &b, int64_t &Pb) {
+  int64_t carry = 0;
+  b = -1;
+  Pb = 0;
+  for (int b0 = 0; b0 < P.B && b < 0; b0 += 64) {
+    int lo;
+    const int nk = b0 + lane < P.B ? row_keys(P, b0 + lane, lo) : 0;
+    const int64_t tot = int64_t(nk) * P.n_units;
+    const int64_t incl = scan_incl_i64(tot, lane);
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(carry + incl > x);
+    if (hit) {
+      const int l0 = __builtin_ctzll(hit);
+      b = b0 + l0;
+      Pb = carry + shfl_i64(incl - tot, l0);
+    }
+    carry += shfl_i64(incl, 63);
+  }
+}
+
+// LDS image of one wave's accumulators at the end of a segment: o[row][head][D], m, l.
+struct WaveAcc {
+  float o[KG][GM][D];
+  float m[KG][GM];
+  float l[KG][GM];
+};
+
+__global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
+  __shared__ WaveAcc s_acc[4];
+  __shared__ int s_prev;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;  // wave within the workgroup
+  const int g = blockIdx.x;
+  const int r = lane >> 4;  // KV head within the unit's group of four
+  const int c = lane & 15;  // 16-byte column of the head row
+
+  // Rows outside the cache: NaN output, written by workgroup b % n_groups.
+  for (int b = g; b < P.B; b += P.n_groups) {
+    int lo;
+    if (row_keys(P, b, lo) == 0)
+      for (int i = threadIdx.x; i < P.H * D; i += 256) P.out[int64_t(b) * P.H * D + i] = 0x7fc0;
+  }
+  const int64_t T = slots_before(P, P.B, lane);
+  // NG <= T active workgroups: every range [g*T/NG, (g+1)*T/NG) is then non-empty, so the
+  // workgroups spanning a unit are exactly those from its first slot's owner to its last.
+  const int NG = int(min(int64_t(P.n_groups), T));
+  if (g >= NG) return;
+  const int64_t start = int64_t(g) * T / NG;
+  const int64_t end = int64_t(g + 1) * T / NG;
+  int b;
+  int64_t Pb;
+  find_row(P, start, lane, b, Pb);
+
+  const bool fuse_new = P.k_new != nullptr;
+  const int64_t tok_stride = int64_t(P.H_kv) * D;
+  int64_t x = start;
+  while (x < end) {
+    int lo;
+    const int nk = row_keys(P, b, lo);
+    const int pos = lo + nk - 1;
+    const int64_t off = x - Pb;
+    const int unit = int(off / nk);
+    const int t_rel = int(off - int64_t(unit) * nk);
+    const int seg = int(min(end - x, int64_t(nk - t_rel)));
+    const int ts = lo + t_rel;  // first key of the segment
+    const int last = ts + seg - 1;
+
+    const int kg = unit / P.n_hc;
+    const int hc = unit - kg * P.n_hc;
+    const int kvh_raw = kg * KG + r;
+    const bool row_live = kvh_raw < P.H_kv;
+    const int kvh = row_live ? kvh_raw : P.H_kv - 1;  // idle rows re-read a live head
+    const int h0 = kvh * P.G + hc * GM;
+    const int gcount = row_live ? min(GM, P.G - hc * GM) : 0;
+    const bool append_here = fuse_new && hc == 0 && row_live;
+
+    // Query heads of this lane's KV head, packed bf16 pairs of its 8 dims (zero past gcount).
+    uint4 qv[GM];
+#pragma unroll
+    for (int h = 0; h < GM; ++h)
+      qv[h] = h < gcount ? *reinterpret_cast<const uint4 *>(P.q + (int64_t(b) * P.H + h0 + h) * D + c * 8)
+                         : make_uint4(0, 0, 0, 0);
+
+    const uint16_t *kbase = P.k_cache + int64_t(b) * P.cache_b + int64_t(kvh) * D + c * 8;
+    const uint16_t *vbase = P.v_cache + int64_t(b) * P.cache_b + int64_t(kvh) * D + c * 8;
+    const int64_t new_off = (int64_t(b) * P.H_kv + kvh) * D + c * 8;
+
+    // Loads are unconditional (keys past the segment re-read its last key and are masked), so
+    // the prefetch of the next tile is straight-line code and stays in flight.
+    auto load_tile = [&](Tile &Tl, int tile) {
+#pragma unroll
+      for (int j = 0; j < kTokens; ++j) {
+        const int t = min(ts + tile * kTokens + j, last);
+        const bool is_new = fuse_new && t == pos;
+        const uint16_t *kp = is_new ? P.k_new + new_off : kbase + int64_t(t) * tok_stride;
+        const uint16_t *vp = is_new ? P.v_new + new_off : vbase + int64_t(t) * tok_stride;
+        Tl.k[j] = *reinterpret_cast<const uint4 *>(kp);
+        Tl.v[j] = *reinterpret_cast<const uint4 *>(vp);
+      }
+    };
+
+    float m = -INFINITY;  // running max (exp2 domain) of this lane's head c%4
+    float l = 0.f;        // this lane's own sum of weights
+    float o[GM][8];
+#pragma unroll
+    for (int h = 0; h < GM; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+
+    auto process = [&](const Tile &Tl, int tile) {
+      if (append_here && pos <= last) {
+#pragma unroll
+        for (int j = 0; j < kTokens; ++j) {
+          if (ts + tile * kTokens + j == pos) {
+            const int64_t at = int64_t(b) * P.cache_b + int64_t(pos) * tok_stride + int64_t(kvh) * D + c * 8;
+            *reinterpret_cast<uint4 *>(P.k_cache + at) = Tl.k[j];
+            *reinterpret_cast<uint4 *>(P.v_cache + at) = Tl.v[j];
+          }
+        }
+      }
+      // Partial scores xs[4j + h] over this lane's 8 dims.
+      float xs[16];
+#pragma unroll
+      for (int j = 0; j < kTokens; ++j) {
+#pragma unroll
+        for (int h = 0; h < GM; ++h) {
+          float a = dot2(Tl.k[j].x, qv[h].x, 0.f);
+          a = dot2(Tl.k[j].y, qv[h].y, a);
+          a = dot2(Tl.k[j].z, qv[h].z, a);
+          a = dot2(Tl.k[j].w, qv[h].w, a);
+          xs[4 * j + h] = a;
+        }
+      }
+      // Reduce-scatter over the row: lane c ends with value index c = 4j + h.
+      rs_step<8, kRowMirror>(xs, c >= 8);
+      rs_step<4, kRowHalfMirror>(xs, (c & 7) >= 4);
+      rs_step<2, kQuadSwap3>(xs, (c & 3) >= 2);
+      rs_step<1, kQuadSwap1>(xs, (c & 1) != 0);
+      const int tt = tile * kTokens + (c >> 2);
+      const float sc = tt < seg ? xs[0] * P.scale_log2 : -INFINITY;
+
+      // Maximum per head over the tile: lanes c, c+4, c+8, c+12 share head c%4.
+      float mx = fmaxf(sc, dpp<kRowRor4>(sc));
+      mx = fmaxf(mx, dpp<kRowRor8>(mx));
+      if (__builtin_amdgcn_ballot_w64(mx > m + kRescaleSlack) != 0) {
+        const float m_new = fmaxf(m, mx);
+        const float alpha = m_new == -INFINITY ? 1.f : exp2_or_zero(m - m_new);
+        l *= alpha;
+        const float a0 = quad_bcast<0>(alpha), a1 = quad_bcast<1>(alpha);
+        const float a2 = quad_bcast<2>(alpha), a3 = quad_bcast<3>(alpha);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          o[0][e] *= a0;
+          o[1][e] *= a1;
+          o[2][e] *= a2;
+          o[3][e] *= a3;
+        }
+        m = m_new;
+      }
+      const float p = sc == -INFINITY ? 0.f : fast_exp2(sc - m);
+      l += p;
+
+      // Weights of the tile's 4 tokens x 4 heads, packed as (token 2i, token 2i+1) pairs.
+      uint32_t pp[GM][2];
+      pp[0][0] = pack_bf16(dpp<kRowNewBcast + 0>(p), dpp<kRowNewBcast + 4>(p));
+      pp[1][0] = pack_bf16(dpp<kRowNewBcast + 1>(p), dpp<kRowNewBcast + 5>(p));
+      pp[2][0] = pack_bf16(dpp<kRowNewBcast + 2>(p), dpp<kRowNewBcast + 6>(p));
+      pp[3][0] = pack_bf16(dpp<kRowNewBcast + 3>(p), dpp<kRowNewBcast + 7>(p));
+      pp[0][1] = pack_bf16(dpp<kRowNewBcast + 8>(p), dpp<kRowNewBcast + 12>(p));
+      pp[1][1] = pack_bf16(dpp<kRowNewBcast + 9>(p), dpp<kRowNewBcast + 13>(p));
+      pp[2][1] = pack_bf16(dpp<kRowNewBcast + 10>(p), dpp<kRowNewBcast + 14>(p));
+      pp[3][1] = pack_bf16(dpp<kRowNewBcast + 11>(p), dpp<kRowNewBcast + 15>(p));
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) {
+        const uint4 va = Tl.v[2 * pr], vb = Tl.v[2 * pr + 1];
+        const uint32_t wa[4] = {va.x, va.y, va.z, va.w};
+        const uint32_t wb[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t even = __builtin_amdgcn_perm(wb[q], wa[q], 0x05040100u);  // dim 2q
+          const uint32_t odd = __builtin_amdgcn_perm(wb[q], wa[q], 0x07060302u);   // dim 2q+1
+#pragma unroll
+          for (int h = 0; h < GM; ++h) {
+            o[h][2 * q] = dot2(even, pp[h][pr], o[h][2 * q]);
+            o[h][2 * q + 1] = dot2(odd, pp[h][pr], o[h][2 * q + 1]);
+          }
+        }
+      }
+    };
+
+    // The workgroup's four waves share the segment: wave wv takes tiles wv, wv + 4, ..., two per
+    // trip, ping-ponging between A and Bt; tiles past the segment are fully masked.
+    const int ntile = (seg + kTokens - 1) / kTokens;
+    Tile A, Bt;
+    load_tile(A, wv);
+    for (int tile = wv; tile < ntile; tile += 8) {
+      load_tile(Bt, tile + 4);
+      process(A, tile);
+      load_tile(A, tile + 8);
+      process(Bt, tile + 4);
+    }
+
+    // Per-head totals of this wave: l summed over the four lanes of head c%4, then every lane
+    // takes the (m, l) of all four heads of its row from its quad. Into LDS for the merge.
+    l += dpp<kRowRor4>(l);
+    l += dpp<kRowRor8>(l);
+    WaveAcc &mine = s_acc[wv];
+#pragma unroll
+    for (int h = 0; h < GM; ++h) {
+      *reinterpret_cast<float4 *>(&mine.o[r][h][c * 8]) = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+      *reinterpret_cast<float4 *>(&mine.o[r][h][c * 8 + 4]) = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+    }
+    if (c < GM) {  // lane c of the row holds head c's (m, l)
+      mine.m[r][c] = m;
+      mine.l[r][c] = l;
+    }
+    __syncthreads();
+
+    // Merge the four waves: wave wv now owns KV-head row wv; lane (h, c) = (lane / 16, lane % 16)
+    // owns head h and dims c*8..c*8+7 of that row.
+    const int mr = wv;
+    const int mh = lane >> 4;
+    float M = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) M = fmaxf(M, s_acc[u].m[mr][mh]);
+    float L = 0.f, acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float wgt = exp2_or_zero(s_acc[u].m[mr][mh] - M);
+      L += s_acc[u].l[mr][mh] * wgt;
+      const float4 a = *reinterpret_cast<const float4 *>(&s_acc[u].o[mr][mh][c * 8]);
+      const float4 bq = *reinterpret_cast<const float4 *>(&s_acc[u].o[mr][mh][c * 8 + 4]);
+      acc[0] = fmaf(a.x, wgt, acc[0]);
+      acc[1] = fmaf(a.y, wgt, acc[1]);
+      acc[2] = fmaf(a.z, wgt, acc[2]);
+      acc[3] = fmaf(a.w, wgt, acc[3]);
+      acc[4] = fmaf(bq.x, wgt, acc[4]);
+      acc[5] = fmaf(bq.y, wgt, acc[5]);
+      acc[6] = fmaf(bq.z, wgt, acc[6]);
+      acc[7] = fmaf(bq.w, wgt, acc[7]);
+    }
+
+    // This row's output heads (a row past H_kv writes nothing).
+    const int m_kvh = kg * KG + mr;
+    const bool m_live = m_kvh < P.H_kv && mh < min(GM, P.G - hc * GM);
+    uint16_t *out_at = P.out + (int64_t(b) * P.H + int64_t(m_kvh) * P.G + hc * GM + mh) * D + c * 8;
+    auto write_out = [&](const float (&v)[8], float denom) {
+      const float inv = 1.f / denom;
+      uint4 v4;
+      v4.x = pack_bf16(v[0] * inv, v[1] * inv);
+      v4.y = pack_bf16(v[2] * inv, v[3] * inv);
+      v4.z = pack_bf16(v[4] * inv, v[5] * inv);
+      v4.w = pack_bf16(v[6] * inv, v[7] * inv);
+      *reinterpret_cast<uint4 *>(out_at) = v4;
+    };
+
+    const int ug = b * P.n_units + unit;
+    const int64_t unit_start = Pb + int64_t(unit) * nk;
+    const int g_first = group_of(unit_start, T, NG);
+    const int g_last = group_of(unit_start + nk - 1, T, NG);
+    if (g_first == g_last) {
+      if (m_live) write_out(acc, L);  // the segment is the whole unit
+    } else {
+      // Publish this workgroup's partial for the unit (slot g + ug, distinct per segment), with
+      // agent-scope stores: partials cross XCDs, each with its own L2. The counter is bumped
+      // once all of them are acknowledged.
+      float *slot = P.part + int64_t(g + ug) * kPart;
+      float *po = slot + (mr * GM + mh) * D + c * 8;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) store_agent2(po + e, acc[e], acc[e + 1]);
+      if (c == 0) store_agent2(slot + KG * GM * D + 2 * (mr * GM + mh), M, L);
+      wait_stores();
+      __syncthreads();
+      int *counter = P.counters + ug;
+      if (threadIdx.x == 0)
+        s_prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      const int nseg = g_last - g_first + 1;
+      if (s_prev == nseg - 1) {
+        // Last workgroup of the unit: merge the nseg partials by log-sum-exp, up to 16 segments'
+        // loads in flight at once.
+        const float *base = P.part + int64_t(g_first + ug) * kPart;
+        float MM = -INFINITY, LL = 0.f, tot[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tot[e] = 0.f;
+        for (int s0 = 0; s0 < nseg; s0 += 16) {
+          float2 ml[16];
+          float2 v[16][4];
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            const float *ps = base + int64_t(s0 + min(k, nseg - 1 - s0)) * kPart;
+            ml[k] = load_agent2(const_cast<float *>(ps) + KG * GM * D + 2 * (mr * GM + mh));
+            const float *pv = ps + (mr * GM + mh) * D + c * 8;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[k][e] = load_agent2(const_cast<float *>(pv) + 2 * e);
+          }
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            // Segments past nseg re-read the last one; they get weight 0 (m = -inf).
+            const float mk = s0 + k < nseg ? ml[k].x : -INFINITY;
+            const float m_new = fmaxf(MM, mk);
+            const float fa = exp2_or_zero(MM - m_new), fb = exp2_or_zero(mk - m_new);
+            LL = LL * fa + ml[k].y * fb;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              tot[2 * e] = tot[2 * e] * fa + v[k][e].x * fb;
+              tot[2 * e + 1] = tot[2 * e + 1] * fa + v[k][e].y * fb;
+            }
+            MM = m_new;
+          }
+        }
+        if (m_live) write_out(tot, LL);
+        if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __syncthreads();  // s_acc and s_prev are reused by the next segment
+
+    // Next segment: the next unit of this row, or the next row that has keys.
+    x += seg;
+    if (x == Pb + int64_t(nk) * P.n_units) {
+      Pb = x;
+      int lo2;
+      do {
+        ++b;
+      } while (b < P.B && row_keys(P, b, lo2) == 0);
+    }
+  }
+}
+
+// Number of compute units of the current device (queried once per device).
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+}  // namespace
+
+int64_t decode_fused_units(int64_t n_head, int64_t n_kv_head) {
+  const int64_t G = n_head / n_kv_head;
+  return ((n_kv_head + KG - 1) / KG) * ((G + GM - 1) / GM);
+}
+
+size_t decode_fused_partial_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head,
+                                  int64_t t_max, int64_t window) {
+  (void)t_max;
+  (void)window;
+  return size_t((kMaxGroups + batch * decode_fused_units(n_head, n_kv_head)) * kPart * 4);
+}
+
+bool decode_fused_supported(const AttnArgs &a) {
+  return a.dtype == MCAMD_BF16 && a.head_dim == D &&
+         a.batch * decode_fused_units(a.n_head, a.n_kv_head) <= kMaxCounters;
+}
+
+int launch_decode_fused(const AttnArgs &a) {
+  FusedParams P;
+  P.q = static_cast<const uint16_t *>(a.q);
+  P.k_new = static_cast<const uint16_t *>(a.k_new);
+  P.v_new = static_cast<const uint16_t *>(a.v_new);
+  P.k_cache = static_cast<uint16_t *>(const_cast<void *>(a.k_cache));
+  P.v_cache = static_cast<uint16_t *>(const_cast<void *>(a.v_cache));
+  P.seqlens = a.seqlens;
+  P.out = static_cast<uint16_t *>(a.out);
+  P.B = int(a.batch);
+  P.H = int(a.n_head);
+  P.H_kv = int(a.n_kv_head);
+  P.G = int(a.n_head / a.n_kv_head);
+  P.n_hc = (P.G + GM - 1) / GM;
+  P.n_kg = (P.H_kv + KG - 1) / KG;
+  P.n_units = P.n_kg * P.n_hc;
+  P.T_max = int(a.t_max);
+  P.window = int(a.window < 0 ? -1 : a.window);
+  P.cache_b = a.cache_batch_stride;
+  P.scale_log2 = float(kLog2e / std::sqrt(double(D)));
+  // Workgroups: one per CU, but no more than one per kMinKeysPerGroup slots of the largest total.
+  const int64_t span = a.window >= 0 ? std::min<int64_t>(a.t_max, a.window + 1) : a.t_max;
+  const int64_t t_upper = a.batch * P.n_units * span;
+  int64_t groups = std::min<int64_t>(int64_t(device_cus()) * kGroupsPerCU, kMaxGroups);
+  groups = std::max<int64_t>(1, std::min<int64_t>(groups, (t_upper + kMinKeysPerGroup - 1) / kMinKeysPerGroup));
+  P.n_groups = int(groups);
+  char *ws = static_cast<char *>(a.workspace);
+  P.counters = reinterpret_cast<int *>(ws);
+  P.part = reinterpret_cast<float *>(ws + kCounterRegionBytes);
+  hipLaunchKernelGGL(decode_fused_kernel, dim3(unsigned(groups)), dim3(256), 0, a.stream, P);
+  return launch_status("decode_fused");
+}
+
+}  // namespace mcamd

@@ -277,11 +277,15 @@ int64_t decode_max_splits(int64_t t_max, int64_t window) {
   return (span + SL - 1) / SL;
 }
 
-size_t decode_workspace_bytes(int64_t batch, int64_t n_head, int64_t head_dim, int64_t t_max,
-                              int64_t window) {
+size_t decode_workspace_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
+                              int64_t t_max, int64_t window) {
   const int64_t ns = decode_max_splits(t_max, window);
-  const int64_t floats = batch * n_head * ns * (head_dim + 2);
-  return size_t((floats * 4 + 255) / 256 * 256);
+  const size_t generic = size_t(batch * n_head * ns * (head_dim + 2) * 4);
+  // The fused path serves head_dim 128 (bf16); other head dims only ever take the general one.
+  const size_t fused =
+      head_dim == 128 ? decode_fused_partial_bytes(batch, n_head, n_kv_head, t_max, window) : 0;
+  const size_t part = generic > fused ? generic : fused;
+  return kCounterRegionBytes + (part + 255) / 256 * 256;
 }
 
 int launch_decode(const AttnArgs &a) {
@@ -291,6 +295,15 @@ int launch_decode(const AttnArgs &a) {
   if (a.batch == 0) {
     clear_error();
     return MCAMD_OK;
+  }
+  if (decode_fused_supported(a)) return launch_decode_fused(a);
+  if (a.k_new) {
+    // The general-shape kernels read the cache only: append first.
+    AppendArgs ap{a.k_new, a.v_new, const_cast<void *>(a.k_cache), const_cast<void *>(a.v_cache),
+                  a.seqlens, a.batch, 1, a.n_kv_head, a.head_dim, a.t_max, a.cache_batch_stride,
+                  a.dtype, a.stream};
+    st = launch_append(ap);
+    if (st != MCAMD_OK) return st;
   }
   DecodeParams P;
   P.q = a.q;
@@ -311,7 +324,8 @@ int launch_decode(const AttnArgs &a) {
   P.cache_b = a.cache_batch_stride;
   P.scale_log2 = float(kLog2e / std::sqrt(double(a.head_dim)));
   const int64_t floats_o = a.batch * a.n_head * P.n_splits * a.head_dim;
-  P.part_o = static_cast<float *>(a.workspace);
+  P.k_new = P.v_new = nullptr;  // appended above
+  P.part_o = reinterpret_cast<float *>(static_cast<char *>(a.workspace) + kCounterRegionBytes);
   P.part_ml = P.part_o + floats_o;
   if (a.dtype == MCAMD_BF16) return dispatch_d<bf16>(P, int(a.batch), a.stream);
   return dispatch_d<float>(P, int(a.batch), a.stream);

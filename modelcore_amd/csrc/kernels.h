@@ -35,8 +35,20 @@ int launch_prefill(const AttnArgs &a);
 // Split-K geometry of the decode path: keys per split and the number of splits a row can need.
 constexpr int kDecodeSplitLen = 256;
 int64_t decode_max_splits(int64_t t_max, int64_t window);
-size_t decode_workspace_bytes(int64_t batch, int64_t n_head, int64_t head_dim, int64_t t_max,
-                              int64_t window);
+
+// Workspace layout of the decode path: a fixed region of merge counters first (zero when the
+// workspace is handed over, and left zero by every call), then the split partials.
+constexpr size_t kCounterRegionBytes = 64 * 1024;
+constexpr int64_t kMaxCounters = int64_t(kCounterRegionBytes / 4);
+size_t decode_workspace_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
+                              int64_t t_max, int64_t window);
+
+// The fused bf16 / head_dim 128 decode (append + split-K + merge in one launch).
+bool decode_fused_supported(const AttnArgs &a);
+int launch_decode_fused(const AttnArgs &a);
+int64_t decode_fused_units(int64_t n_head, int64_t n_kv_head);
+size_t decode_fused_partial_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head,
+                                  int64_t t_max, int64_t window);
 
 // Shape checks shared by every attention entry point.
 int check_attn_shapes(const AttnArgs &a, bool need_workspace);

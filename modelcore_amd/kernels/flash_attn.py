@@ -147,12 +147,13 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
     lib = _ext.lib()
     w = _window(window_size)
     ws_bytes = lib.mcamd_attn_workspace_bytes(B, T_new, H, H_kv, D, T_max, w)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    ws = _ext.workspace(q.device, ws_bytes)
     st = lib.mcamd_flash_attn_with_kvcache(
         q.data_ptr(), k.data_ptr() if k is not None else None,
         v.data_ptr() if v is not None else None, k_cache.data_ptr(), v_cache.data_ptr(),
         seqlens.data_ptr(), out.data_ptr(), B, T_new, H, H_kv, D, T_max, k_cache.stride(0), w,
-        int(bool(causal)), code, ws.data_ptr() if ws is not None else None, ws_bytes,
+        int(bool(causal)), code, ws.data_ptr() if ws is not None else None,
+        ws.numel() if ws is not None else 0,
         _ext.stream_handle(q.device))
     _ext.check(st, "flash_attn_with_kvcache")
     return out

@@ -155,6 +155,11 @@ DECODE_CASES = [
     ([9, 30], 2, 2, 16, 40, 8),
     ([60, 3], 16, 2, 64, 64, -1),   # G = 8
     ([60, 3], 16, 1, 64, 64, 0),    # G = 16: two head chunks; window 0
+    ([300, 5, 777], 16, 2, 128, 800, -1),   # G = 8 at head_dim 128: two 4-head groups
+    ([1030, 2], 16, 1, 128, 1040, 200),     # G = 16 at head_dim 128, windowed
+    ([4095, 17], 4, 4, 128, 4100, 1024),    # MHA, 4 windowed splits
+    ([0, 3], 16, 4, 128, 2000, -1),         # far fewer keys than waves
+    ([1999, 0, 1], 16, 4, 128, 2000, 5),    # tiny windows in a long cache
 ]
 
 
@@ -169,6 +174,59 @@ def test_decode_matches_the_oracle(dtype, seqlens, H, H_kv, D, T_max, window):
     assert err <= ATOL[dtype], f"max-abs {err}"
     ek, _ = ko.append(bits(c["k_cache"]), bits(c["v_cache"]), bits(c["k"]), bits(c["v"]), seqlens)
     assert np.array_equal(bits(g["k_cache"]), ek)
+
+
+def test_repeated_decode_calls_are_deterministic():
+    """The split merge counts arrivals in the workspace and resets the counters: repeated calls,
+    also after a call of another shape on the same workspace, give identical bits."""
+    c = make_case([700, 31, 2000, 256], 1, 16, 4, 128, 2100, torch.bfloat16, seed=23)
+    first, _ = _run_op(c, -1)
+    other = make_case([90, 1500], 1, 32, 8, 128, 1600, torch.bfloat16, seed=24)
+    _run_op(other, 64)
+    for _ in range(3):
+        again, _ = _run_op(c, -1)
+        assert torch.equal(first, again)
+    assert max_abs(to_np(first), _oracle(c, -1)) <= ATOL[torch.bfloat16]
+
+
+def test_decode_replayed_from_a_hip_graph_matches_eager():
+    """A captured decode step (append + attention) replayed several times, with eager work and
+    synchronisations between the replays, matches the eager result of the same step each time."""
+    c = make_case([513, 64, 1999], 1, 16, 4, 128, 2048, torch.bfloat16, seed=25)
+    g = _gpu(c)
+    kc0, vc0 = g["k_cache"].clone(), g["v_cache"].clone()
+
+    def step():
+        return flash_attn.flash_attn_with_kvcache(g["q"], g["k_cache"], g["v_cache"], k=g["k"],
+                                                  v=g["v"], cache_seqlens=g["cache_seqlens"],
+                                                  causal=True, window_size=(-1, 0))
+
+    eager = step().clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step()
+    for i in range(4):
+        g["k_cache"].copy_(kc0)
+        g["v_cache"].copy_(vc0)
+        _run_op(make_case([40], 1, 8, 2, 128, 64, torch.bfloat16, seed=26 + i), -1)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        assert torch.equal(g["k_cache"][0, 513].cpu(), c["k"][0, 0])
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_rows_past_the_cache_get_nan_and_leave_the_cache_alone(D):
+    """A row whose position is outside the cache cannot be attended (the reference raises an
+    index error there): its output is NaN, its cache row is untouched, other rows are exact."""
+    seqlens = [64, 10, 63]
+    c = make_case(seqlens, 1, 8, 2, D, 64, torch.bfloat16, seed=27)
+    out, g = _run_op(c, -1)
+    assert torch.isnan(out[0].float()).all()
+    assert torch.equal(g["k_cache"][0].cpu(), c["k_cache"][0])
+    ok = {k: v[1:] for k, v in c.items()}
+    assert max_abs(to_np(out[1:]), _oracle(ok, -1)) <= ATOL[torch.bfloat16]
 
 
 def test_decode_without_append_reads_the_cache():
