@@ -49,8 +49,15 @@ constexpr int KG = 4;                 // KV heads per unit (one per row of 16 la
 constexpr int kTokens = 4;            // tokens per tile
 constexpr float kRescaleSlack = 8.f;  // log2 units
 constexpr int kMaxGroups = 1024;      // 4-wave workgroups per launch, at most
-constexpr int kGroupsPerCU = 1;       // one wave per SIMD
+#ifndef MCAMD_DECODE_GROUPS_PER_CU
+#define MCAMD_DECODE_GROUPS_PER_CU 1
+#endif
+constexpr int kGroupsPerCU = MCAMD_DECODE_GROUPS_PER_CU;  // 1: one wave per SIMD
 constexpr int kMinKeysPerGroup = 256; // fewer workgroups when the whole job is small
+#ifndef MCAMD_DECODE_RING
+#define MCAMD_DECODE_RING 2
+#endif
+constexpr int kRing = MCAMD_DECODE_RING;  // tile buffers per wave (kRing - 1 tiles in flight)
 constexpr int kPart = KG * GM * D + 2 * KG * GM;  // floats per partial: o[16][D], (m, l)[16]
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -61,8 +68,7 @@ struct FusedParams {
   uint16_t *k_cache, *v_cache;
   const int32_t *seqlens;
   uint16_t *out;
-  float *part;    // [n_groups + B * n_units][kPart]: segment partials, slot = group + unit
-  int *counters;  // [B * n_units]: partials of the unit published so far (zero between calls)
+  float *part;  // [n_groups + B * n_units][kPart]: segment partials, slot = group + unit
   int B, H, H_kv, G, n_hc, n_kg, n_units, T_max, window, n_groups;
   int64_t cache_b;
   float scale_log2;
@@ -137,18 +143,6 @@ __device__ __forceinline__ int group_of(int64_t x, int64_t T, int NG) {
   return int(((x + 1) * NG + T - 1) / T - 1);
 }
 
-// Agent-scope (coherent across XCDs) relaxed accesses for the cross-workgroup partials.
-__device__ __forceinline__ void store_agent2(float *p, float a, float b) {
-  const uint64_t v = (uint64_t(__float_as_uint(b)) << 32) | __float_as_uint(a);
-  __hip_atomic_store(reinterpret_cast<uint64_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float2 load_agent2(float *p) {
-  const uint64_t v =
-      __hip_atomic_load(reinterpret_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return make_float2(__uint_as_float(uint32_t(v)), __uint_as_float(uint32_t(v >> 32)));
-}
-// s_waitcnt vmcnt(0): every store of this wave has been acknowledged.
-__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 __device__ __forceinline__ int64_t shfl_i64(int64_t v, int src) {
   const int lo = __shfl(int(uint64_t(v)), src, 64);
@@ -203,9 +197,113 @@ struct WaveAcc {
   float l[KG][GM];
 };
 
+__device__ __forceinline__ void write_bf16x8(uint16_t *at, const float (&v)[8], float denom) {
+  const float inv = 1.f / denom;
+  uint4 v4;
+  v4.x = pack_bf16(v[0] * inv, v[1] * inv);
+  v4.y = pack_bf16(v[2] * inv, v[3] * inv);
+  v4.z = pack_bf16(v[4] * inv, v[5] * inv);
+  v4.w = pack_bf16(v[6] * inv, v[7] * inv);
+  *reinterpret_cast<uint4 *>(at) = v4;
+}
+
+// Merge of the nseg partials of unit ug (slots g_first + ug ...) by log-sum-exp, run by a
+// whole workgroup: wave wv takes KV-head row wv, lane (h, c) = (lane / 16, lane % 16) head h and
+// dims c*8..c*8+7. Up to 16 segments' loads are in flight at once.
+__device__ void merge_unit(const FusedParams &P, int ug, int g_first, int nseg) {
+  const int lane = threadIdx.x & 63;
+  const int mr = threadIdx.x >> 6;
+  const int mh = lane >> 4;
+  const int c = lane & 15;
+  const int b = ug / P.n_units;
+  const int unit = ug - b * P.n_units;
+  const int kg = unit / P.n_hc;
+  const int hc = unit - kg * P.n_hc;
+  const int kvh = kg * KG + mr;
+  const float *base = P.part + int64_t(g_first + ug) * kPart;
+  float MM = -INFINITY, LL = 0.f, tot[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) tot[e] = 0.f;
+  for (int s0 = 0; s0 < nseg; s0 += 16) {
+    float2 ml[16];
+    float2 v[16][4];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float *ps = base + int64_t(s0 + min(k, nseg - 1 - s0)) * kPart;
+      ml[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * (mr * GM + mh));
+      const float *pv = ps + (mr * GM + mh) * D + c * 8;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[k][e] = *reinterpret_cast<const float2 *>(pv + 2 * e);
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      // Segments past nseg re-read the last one; they get weight 0 (m = -inf).
+      const float mk = s0 + k < nseg ? ml[k].x : -INFINITY;
+      const float m_new = fmaxf(MM, mk);
+      const float fa = exp2_or_zero(MM - m_new), fb = exp2_or_zero(mk - m_new);
+      LL = LL * fa + ml[k].y * fb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        tot[2 * e] = tot[2 * e] * fa + v[k][e].x * fb;
+        tot[2 * e + 1] = tot[2 * e + 1] * fa + v[k][e].y * fb;
+      }
+      MM = m_new;
+    }
+  }
+  if (kvh < P.H_kv && mh < min(GM, P.G - hc * GM))
+    write_bf16x8(P.out + (int64_t(b) * P.H + int64_t(kvh) * P.G + hc * GM + mh) * D + c * 8, tot, LL);
+}
+
+// This workgroup's share of the slots: total T, active workgroups NG = min(n_groups, T), the
+// range [start, end), and the row b holding `start` with Pb its first slot. One read of
+// cache_seqlens when B <= 64.
+__device__ void locate(const FusedParams &P, int g, int lane, int64_t &T, int &NG, int64_t &start,
+                       int64_t &end, int &b, int64_t &Pb) {
+  if (P.B <= 64) {
+    int lo;
+    const int nk = lane < P.B ? row_keys(P, lane, lo) : 0;
+    const int64_t tot = int64_t(nk) * P.n_units;
+    const int64_t incl = scan_incl_i64(tot, lane);
+    T = shfl_i64(incl, 63);
+    NG = int(min(int64_t(P.n_groups), T));
+    if (g >= NG) return;
+    start = int64_t(g) * T / NG;
+    end = int64_t(g + 1) * T / NG;
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(incl > start);
+    b = __builtin_ctzll(hit);
+    Pb = shfl_i64(incl - tot, b);
+    return;
+  }
+  T = slots_before(P, P.B, lane);
+  NG = int(min(int64_t(P.n_groups), T));
+  if (g >= NG) return;
+  start = int64_t(g) * T / NG;
+  end = int64_t(g + 1) * T / NG;
+  find_row(P, start, lane, b, Pb);
+}
+
+// Geometry of row b for the merge pass: total slots T, active workgroups NG, first slot Pb of
+// row b and its key range start lo; returns the row's key count (0: nothing to merge).
+__device__ int row_geometry(const FusedParams &P, int b, int lane, int64_t &T, int &NG,
+                            int64_t &Pb, int &lo) {
+  const int nk = row_keys(P, b, lo);
+  if (P.B <= 64) {
+    int lo2;
+    const int nkl = lane < P.B ? row_keys(P, lane, lo2) : 0;
+    const int64_t tot = int64_t(nkl) * P.n_units;
+    const int64_t incl = scan_incl_i64(tot, lane);
+    T = shfl_i64(incl, 63);
+    Pb = shfl_i64(incl - tot, b);
+  } else {
+    T = slots_before(P, P.B, lane);
+    Pb = slots_before(P, b, lane);
+  }
+  NG = int(min(int64_t(P.n_groups), T));
+  return nk;
+}
+
 __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
   __shared__ WaveAcc s_acc[4];
-  __shared__ int s_prev;
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;  // wave within the workgroup
   const int g = blockIdx.x;
@@ -218,16 +316,12 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
     if (row_keys(P, b, lo) == 0)
       for (int i = threadIdx.x; i < P.H * D; i += 256) P.out[int64_t(b) * P.H * D + i] = 0x7fc0;
   }
-  const int64_t T = slots_before(P, P.B, lane);
   // NG <= T active workgroups: every range [g*T/NG, (g+1)*T/NG) is then non-empty, so the
   // workgroups spanning a unit are exactly those from its first slot's owner to its last.
-  const int NG = int(min(int64_t(P.n_groups), T));
+  int64_t T, start = 0, end = 0, Pb = 0;
+  int NG, b = 0;
+  locate(P, g, lane, T, NG, start, end, b, Pb);
   if (g >= NG) return;
-  const int64_t start = int64_t(g) * T / NG;
-  const int64_t end = int64_t(g + 1) * T / NG;
-  int b;
-  int64_t Pb;
-  find_row(P, start, lane, b, Pb);
 
   const bool fuse_new = P.k_new != nullptr;
   const int64_t tok_stride = int64_t(P.H_kv) * D;
@@ -366,16 +460,21 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
       }
     };
 
-    // The workgroup's four waves share the segment: wave wv takes tiles wv, wv + 4, ..., two per
-    // trip, ping-ponging between A and Bt; tiles past the segment are fully masked.
+    // The workgroup's four waves share the segment: wave wv takes tiles wv, wv + 4, ... . A ring
+    // of kRing tile buffers keeps kRing - 1 tiles' loads in flight while one is consumed (with
+    // one wave per SIMD, this prefetch depth is what hides the memory latency).
     const int ntile = (seg + kTokens - 1) / kTokens;
-    Tile A, Bt;
-    load_tile(A, wv);
-    for (int tile = wv; tile < ntile; tile += 8) {
-      load_tile(Bt, tile + 4);
-      process(A, tile);
-      load_tile(A, tile + 8);
-      process(Bt, tile + 4);
+    Tile ring[kRing];
+#pragma unroll
+    for (int i = 0; i < kRing - 1; ++i) load_tile(ring[i], wv + 4 * i);
+    for (int tile = wv; tile < ntile; tile += 4 * kRing) {
+#pragma unroll
+      for (int u = 0; u < kRing; ++u) {
+        const int cur = tile + 4 * u;
+        if (cur >= ntile) break;
+        load_tile(ring[(u + kRing - 1) % kRing], cur + 4 * (kRing - 1));
+        process(ring[u], cur);
+      }
     }
 
     // Per-head totals of this wave: l summed over the four lanes of head c%4, then every lane
@@ -441,59 +540,15 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
     if (g_first == g_last) {
       if (m_live) write_out(acc, L);  // the segment is the whole unit
     } else {
-      // Publish this workgroup's partial for the unit (slot g + ug, distinct per segment), with
-      // agent-scope stores: partials cross XCDs, each with its own L2. The counter is bumped
-      // once all of them are acknowledged.
+      // This workgroup's partial for the unit: slot g + ug, distinct for every segment. The
+      // merge kernel, launched next on the same stream, combines a unit's partials.
       float *slot = P.part + int64_t(g + ug) * kPart;
       float *po = slot + (mr * GM + mh) * D + c * 8;
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) store_agent2(po + e, acc[e], acc[e + 1]);
-      if (c == 0) store_agent2(slot + KG * GM * D + 2 * (mr * GM + mh), M, L);
-      wait_stores();
-      __syncthreads();
-      int *counter = P.counters + ug;
-      if (threadIdx.x == 0)
-        s_prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __syncthreads();
-      const int nseg = g_last - g_first + 1;
-      if (s_prev == nseg - 1) {
-        // Last workgroup of the unit: merge the nseg partials by log-sum-exp, up to 16 segments'
-        // loads in flight at once.
-        const float *base = P.part + int64_t(g_first + ug) * kPart;
-        float MM = -INFINITY, LL = 0.f, tot[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) tot[e] = 0.f;
-        for (int s0 = 0; s0 < nseg; s0 += 16) {
-          float2 ml[16];
-          float2 v[16][4];
-#pragma unroll
-          for (int k = 0; k < 16; ++k) {
-            const float *ps = base + int64_t(s0 + min(k, nseg - 1 - s0)) * kPart;
-            ml[k] = load_agent2(const_cast<float *>(ps) + KG * GM * D + 2 * (mr * GM + mh));
-            const float *pv = ps + (mr * GM + mh) * D + c * 8;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[k][e] = load_agent2(const_cast<float *>(pv) + 2 * e);
-          }
-#pragma unroll
-          for (int k = 0; k < 16; ++k) {
-            // Segments past nseg re-read the last one; they get weight 0 (m = -inf).
-            const float mk = s0 + k < nseg ? ml[k].x : -INFINITY;
-            const float m_new = fmaxf(MM, mk);
-            const float fa = exp2_or_zero(MM - m_new), fb = exp2_or_zero(mk - m_new);
-            LL = LL * fa + ml[k].y * fb;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              tot[2 * e] = tot[2 * e] * fa + v[k][e].x * fb;
-              tot[2 * e + 1] = tot[2 * e + 1] * fa + v[k][e].y * fb;
-            }
-            MM = m_new;
-          }
-        }
-        if (m_live) write_out(tot, LL);
-        if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      *reinterpret_cast<float4 *>(po) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      *reinterpret_cast<float4 *>(po + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+      if (c == 0) *reinterpret_cast<float2 *>(slot + KG * GM * D + 2 * (mr * GM + mh)) = make_float2(M, L);
     }
-    __syncthreads();  // s_acc and s_prev are reused by the next segment
+    __syncthreads();  // s_acc is reused by the next segment
 
     // Next segment: the next unit of this row, or the next row that has keys.
     x += seg;
@@ -505,6 +560,24 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
       } while (b < P.B && row_keys(P, b, lo2) == 0);
     }
   }
+}
+
+// Merge pass: one workgroup per unit; wave wv takes KV-head row wv of the unit. A unit split over
+// several workgroups of the streaming pass is combined from their partials by log-sum-exp.
+__global__ __launch_bounds__(256) void decode_merge_kernel(FusedParams P) {
+  const int lane = threadIdx.x & 63;
+  const int ug = blockIdx.x;
+  const int b = ug / P.n_units;
+  const int unit = ug - b * P.n_units;
+  int64_t T, Pb;
+  int NG, lo;
+  const int nk = row_geometry(P, b, lane, T, NG, Pb, lo);
+  if (nk == 0) return;
+  const int64_t unit_start = Pb + int64_t(unit) * nk;
+  const int g_first = group_of(unit_start, T, NG);
+  const int g_last = group_of(unit_start + nk - 1, T, NG);
+  if (g_first == g_last) return;  // written directly by the streaming pass
+  merge_unit(P, ug, g_first, g_last - g_first + 1);
 }
 
 // Number of compute units of the current device (queried once per device).
@@ -567,10 +640,13 @@ int launch_decode_fused(const AttnArgs &a) {
   groups = std::max<int64_t>(1, std::min<int64_t>(groups, (t_upper + kMinKeysPerGroup - 1) / kMinKeysPerGroup));
   P.n_groups = int(groups);
   char *ws = static_cast<char *>(a.workspace);
-  P.counters = reinterpret_cast<int *>(ws);
   P.part = reinterpret_cast<float *>(ws + kCounterRegionBytes);
   hipLaunchKernelGGL(decode_fused_kernel, dim3(unsigned(groups)), dim3(256), 0, a.stream, P);
-  return launch_status("decode_fused");
+  int st = launch_status("decode_fused");
+  if (st != MCAMD_OK) return st;
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(unsigned(a.batch * P.n_units)), dim3(256), 0,
+                     a.stream, P);
+  return launch_status("decode_merge");
 }
 
 }  // namespace mcamd
