@@ -26,6 +26,8 @@ METRIC = "decode tok/s at B=32 ctx 8k GQA16/4 hd128; KV path HBM GB/s as % of pe
 B, H, H_KV, D = 32, 16, 4, 128
 L_MIN, L_MAX = 512, 8192
 HBM_PEAK = 8.0e12
+COPY_BYTES = 1 << 30
+TRAFFIC_FILE = "profiles/decode_b32_gqa16x4_hd128_ctx8k_traffic.md"
 
 
 def log(msg):
@@ -40,7 +42,37 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain device copy of COPY_BYTES, ten times (the known-size "
+                         "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
+
+
+def measured_traffic():
+    """HBM bytes per launch of the decode call, as the rocprofv3 FETCH_SIZE and WRITE_SIZE runs
+    recorded them (scaled by the copy calibration) in the committed profile summary, or None."""
+    import re
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_FILE)
+    try:
+        with open(path) as f:
+            m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
+def calibrate_copy():
+    """A plain device-to-device copy of COPY_BYTES, ten times: what FETCH_SIZE and WRITE_SIZE
+    read for a kernel that moves a known number of bytes."""
+    import torch
+    dev = torch.device("cuda", 0)
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_read": COPY_BYTES,
+                      "bytes_written": COPY_BYTES, "launches": 10}), flush=True)
 
 
 def cpu_baseline(kc, vc, q, k, v, seqlens, budget_s=12.0):
@@ -68,6 +100,10 @@ def main():
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the KV path runs per GPU "
               f"with no cross-GPU exchange, so run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
 
     import torch
     from modelcore_amd import _ext, stats
@@ -134,35 +170,39 @@ def main():
     mean_step_bytes = sum(step_bytes) / K
     step_gbps = mean_step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # Dominant kernel: the decode attention (split-K pass + merge), attention only, back to back
-    # on the stream it is launched on, timed with HIP events around N launches.
+    # Dominant kernels: the decode call of one step as the step issues it -- append of the new
+    # token fused into the split-K streaming pass (decode_fused_kernel), then the merge pass
+    # (decode_merge_kernel) -- launched back to back through the C ABI on the stream they run on
+    # and timed with HIP events around N launches. The positions stay put, so every launch
+    # rewrites the same new token and reads the same keys.
     lib = _ext.lib()
     pos = cache.cache_seqlens  # positions now: base + W + K, each row's query at its position
     out = torch.empty(B, 1, H, D, dtype=torch.bfloat16, device=dev)
     ws_bytes = lib.mcamd_attn_workspace_bytes(B, 1, H, H_KV, D, t_alloc, -1)
-    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # merge counters start at zero
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
     stream = _ext.stream_handle(dev)
-    q_attn = qd[0]
+    q1, k1, v1 = qd[0], kd[0], vd[0]
 
-    def attn():
-        return lib.mcamd_decode_attention(q_attn.data_ptr(), k_slot.data_ptr(), v_slot.data_ptr(),
-                                          pos.data_ptr(), out.data_ptr(), B, H, H_KV, D, t_alloc,
-                                          k_slot.stride(0), -1, _ext.BF16, ws.data_ptr(), ws_bytes,
-                                          stream)
+    def decode_call():
+        return lib.mcamd_flash_attn_with_kvcache(
+            q1.data_ptr(), k1.data_ptr(), v1.data_ptr(), k_slot.data_ptr(), v_slot.data_ptr(),
+            pos.data_ptr(), out.data_ptr(), B, 1, H, H_KV, D, t_alloc, k_slot.stride(0), -1, 1,
+            _ext.BF16, ws.data_ptr(), ws_bytes, stream)
 
     for _ in range(5):
-        _ext.check(attn(), "decode_attention")
+        _ext.check(decode_call(), "flash_attn_with_kvcache")
     n_attn = max(K, 50)
     torch.cuda.synchronize()
     start.record()
     for _ in range(n_attn):
-        attn()
+        decode_call()
     end.record()
     torch.cuda.synchronize()
     attn_us = start.elapsed_time(end) / n_attn * 1e3
     attn_positions = final.tolist()
-    attn_bytes = stats.decode_step_bytes(attn_positions, H, H_KV, D, 2, append=False)
+    attn_bytes = stats.decode_step_bytes(attn_positions, H, H_KV, D, 2, append=True)
     attn_gbps = attn_bytes / (attn_us * 1e-6) / 1e9
+    traffic = measured_traffic()
 
     result = {
         "metric": METRIC,
@@ -187,13 +227,13 @@ def main():
         "kv_path_gbps": round(step_gbps, 1),
         "kv_path_pct_peak": round(100 * step_gbps * 1e9 / HBM_PEAK, 2),
         "roofline": {
-            "kernel": "decode_split_kernel + decode_combine_kernel (attention only)",
+            "kernel": "decode_fused_kernel + decode_merge_kernel (append + attention)",
             "bound": "hbm",
             "achieved": round(attn_gbps, 1),
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": round(attn_gbps * 1e9 / HBM_PEAK, 4),
-            "traffic": None,
+            "traffic": traffic,
             "us_per_launch": round(attn_us, 2),
             "bytes_per_launch": attn_bytes,
         },
