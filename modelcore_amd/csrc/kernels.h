@@ -50,6 +50,10 @@ int64_t decode_fused_units(int64_t n_head, int64_t n_kv_head);
 size_t decode_fused_partial_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head,
                                   int64_t t_max, int64_t window);
 
+// The bf16 / head_dim 128 chunked prefill on the matrix cores.
+bool prefill_mfma_supported(const AttnArgs &a);
+int launch_prefill_mfma(const AttnArgs &a);
+
 // Shape checks shared by every attention entry point.
 int check_attn_shapes(const AttnArgs &a, bool need_workspace);
 

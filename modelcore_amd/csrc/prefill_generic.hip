@@ -196,6 +196,7 @@ int launch_prefill(const AttnArgs &a) {
     clear_error();
     return MCAMD_OK;
   }
+  if (prefill_mfma_supported(a)) return launch_prefill_mfma(a);
   return launch_prefill_generic(a);
 }
 

@@ -246,6 +246,14 @@ PREFILL_CASES = [
     ([5, 9], 3, 2, 2, 16, 16, -1),
     ([0], 12, 2, 2, 16, 12, 8),
     ([33, 2], 130, 32, 8, 128, 200, 0),
+    # bf16 / head_dim 128 shapes of the matrix-core kernel: tiles of 64 keys, 256 (position,
+    # head) pairs per workgroup, masks at the diagonal and at window edges inside a tile
+    ([0, 64, 129], 200, 32, 8, 128, 400, -1),     # G = 4, prefixes on and off tile boundaries
+    ([300, 17], 77, 12, 4, 128, 400, 100),        # G = 3 (85 positions per workgroup)
+    ([250], 300, 8, 8, 128, 600, 63),             # MHA, window inside a tile
+    ([5, 400], 40, 16, 2, 128, 448, 64),          # G = 8
+    ([1000], 64, 16, 1, 128, 1100, -1),           # G = 16: 16 positions per workgroup
+    ([7, 0], 1, 32, 8, 128, 16, -1),              # a single query through the prefill path
 ]
 
 
@@ -259,6 +267,41 @@ def test_chunked_prefill_matches_the_oracle(dtype, seqlens, T_new, H, H_kv, D, T
     assert err <= ATOL[dtype], f"max-abs {err}"
     ek, ev = ko.append(bits(c["k_cache"]), bits(c["v_cache"]), bits(c["k"]), bits(c["v"]), seqlens)
     assert np.array_equal(bits(g["k_cache"]), ek) and np.array_equal(bits(g["v_cache"]), ev)
+
+
+def test_chunked_prefill_of_a_long_prompt_at_gqa_32_8():
+    """One 512-token chunk at position 1536 (a 2048-key prefix), 32 q / 8 kv heads, bf16: the
+    chunk shape of the 16384-token chunked-prefill workload, against the float64 oracle."""
+    c = make_case([1536], 512, 32, 8, 128, 2048, torch.bfloat16, seed=33)
+    out, g = _run_op(c, -1)
+    err = max_abs(to_np(out), _oracle(c, -1))
+    assert err <= ATOL[torch.bfloat16], f"max-abs {err}"
+
+
+def test_chunked_prefill_through_the_cache_equals_one_full_prefill():
+    """Feeding a prompt in chunks (append at an offset, attend to the prefix) gives the outputs of
+    one full-prompt call, position by position (modelcore/tests/test_recurrent.py:150-156)."""
+    g = gen(34)
+    B, T, H, H_kv, D, C = 2, 384, 16, 4, 128, 128
+    q = torch.randn(B, T, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn(B, T, H_kv, D, generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn(B, T, H_kv, D, generator=g).to(torch.bfloat16).to(DEV)
+    for window in (-1, 100):
+        full_k = torch.zeros(B, T, H_kv, D, dtype=torch.bfloat16, device=DEV)
+        full_v = torch.zeros_like(full_k)
+        zero = torch.zeros(B, dtype=torch.int32, device=DEV)
+        whole = flash_attn.flash_attn_with_kvcache(q, full_k, full_v, k=k, v=v, cache_seqlens=zero,
+                                                   causal=True, window_size=(window, 0))
+        cache = KVCache(B, H_kv, T, D, 1, DEV, torch.bfloat16)
+        kc, vc = cache.get_slot_cache(0)
+        parts = []
+        for a in range(0, T, C):
+            parts.append(flash_attn.flash_attn_with_kvcache(
+                q[:, a:a + C], kc, vc, k=k[:, a:a + C], v=v[:, a:a + C],
+                cache_seqlens=cache.cache_seqlens, causal=True, window_size=(window, 0)))
+            cache.advance(C)
+        assert torch.equal(kc, full_k) and torch.equal(vc, full_v)
+        assert torch.equal(torch.cat(parts, dim=1), whole), f"window {window}"
 
 
 def test_no_cache_attention_equals_prefill_from_empty():
