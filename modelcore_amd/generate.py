@@ -1,0 +1,78 @@
+"""Generation primitives over the KV path: next-token sampling and the cached ``Decoder``
+(modelcore/generate.py:18-94).
+
+``Decoder`` prefills a prompt at batch 1, replicates its cache into ``num_samples`` rows with the
+HIP replication kernel (``KVCache.prefill``), then steps every row one position per call. Several
+prompts are prefilled one at a time and copied into their own right-ragged rows
+(``KVCache.prefill_row``); row ``p * num_samples + s`` is sample ``s`` of prompt ``p``.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+
+@torch.inference_mode()
+def sample_next_token(logits, rng, temperature=1.0, top_k=None):
+    """(B, vocab) logits -> (B, 1) token ids: argmax at temperature 0, else a multinomial draw
+    from softmax(logits / temperature), over the top_k logits when top_k is set."""
+    assert temperature >= 0.0, "temperature must be non-negative"
+    if temperature == 0.0:
+        return torch.argmax(logits, dim=-1, keepdim=True)
+    if top_k is not None and top_k > 0:
+        vals, idx = torch.topk(logits, min(top_k, logits.size(-1)), dim=-1)
+        choice = torch.multinomial(F.softmax(vals / temperature, dim=-1), num_samples=1,
+                                   generator=rng)
+        return idx.gather(1, choice)
+    return torch.multinomial(F.softmax(logits / temperature, dim=-1), num_samples=1,
+                             generator=rng)
+
+
+class Decoder:
+    """Batch-1 prefill, replication into num_samples rows, then one position per step()."""
+
+    @torch.inference_mode()
+    def __init__(self, model, manager, tokens, *, num_samples=1, max_tokens=None, device=None):
+        self.model = model
+        device = device or model.get_device()
+        if isinstance(tokens[0], int):
+            prefill = manager.new_kv_cache(model, batch_size=1, seq_len=len(tokens), device=device)
+            ids = torch.tensor([tokens], dtype=torch.long, device=device)
+            logits = model.forward(ids, kv_cache=prefill)
+            self._logits = logits[:, -1, :].expand(num_samples, -1)
+            length = len(tokens) + max_tokens if max_tokens is not None \
+                else model.config.sequence_len
+            self.kv_cache = manager.new_kv_cache(model, batch_size=num_samples, seq_len=length,
+                                                 device=device)
+            self.kv_cache.prefill(prefill)
+            return
+        prompts = [list(p) for p in tokens]
+        length = max(map(len, prompts)) + max_tokens if max_tokens is not None \
+            else model.config.sequence_len
+        self.kv_cache = manager.new_kv_cache(model, batch_size=len(prompts) * num_samples,
+                                             seq_len=length, device=device)
+        rows = []
+        for p, prompt in enumerate(prompts):
+            prefill = manager.new_kv_cache(model, batch_size=1, seq_len=len(prompt), device=device)
+            ids = torch.tensor([prompt], dtype=torch.long, device=device)
+            rows.append(model.forward(ids, kv_cache=prefill)[:, -1, :].expand(num_samples, -1))
+            for s in range(num_samples):
+                self.kv_cache.prefill_row(p * num_samples + s, prefill)
+            del prefill
+        self._logits = torch.cat(rows, dim=0)
+
+    @property
+    def logits(self):
+        """Next-token logits (rows, vocab), refreshed by step()."""
+        return self._logits
+
+    @torch.inference_mode()
+    def step(self, token_column):
+        """One next-token id per row (list or (rows,) tensor); advances every row one position."""
+        device = self.model.get_device()
+        if torch.is_tensor(token_column):
+            ids = token_column.to(device=device, dtype=torch.long).view(-1, 1)
+        else:
+            ids = torch.tensor(token_column, dtype=torch.long, device=device).unsqueeze(1)
+        self._logits = self.model.forward(ids, kv_cache=self.kv_cache)[:, -1, :]
+        return self._logits

@@ -1,0 +1,554 @@
+"""The model around the KV path: a config tree, the transformer that calls the cached-attention
+operator, and the ``ModelManager`` surface that builds it and its caches.
+
+This is the caller side of the path (modelcore/model.py, modelcore/components/*,
+modelcore/manager.py:111-119 and :286-299), restated for the architectures the KV path serves:
+token embedding (wte -> compute dtype -> RMSNorm), pre-norm residual blocks whose mixer is GQA
+attention with RoPE (base 100000), parameterless QK RMSNorm and a x1.2 scale on q and k, optional
+sliding windows and cross-layer KV sharing (``kv_slot`` / ``produces_kv``), the ``output_gate``
+feature, gated or plain MLPs, and an lm_head with vocab crop and tanh softcap. The module names
+follow the reference's v3 state-dict keys (``embedding.wte``, ``body.blocks.<i>.mixer.c_q``,
+``body.blocks.<i>.ffn.gate_proj``, ``body.blocks.<i>.mixer.features.output_gate.proj``,
+``unembedding.lm_head``), so a reference state dict loads as is.
+
+Attention goes through ``modelcore_amd.kernels.flash_attn.flash_attn``: the HIP kernels, on a ROCm
+device only. A different operator namespace with the same two functions can be passed as
+``attention=`` (the tests pass the CPU oracle to check this module's own arithmetic on the CPU).
+
+Parameters are created in fp32 and cast to the activation dtype at every matmul, as the reference's
+Linear does (modelcore/components/linear.py:13-14); the token embedding is stored in the compute
+dtype (modelcore/components/embedding.py:64-71).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from modelcore_amd.cache import KVCache
+from modelcore_amd.runtime import Runtime
+
+TYPE_KEY = "#type"
+
+
+# -----------------------------------------------------------------------------------------------
+# Config tree (the subset of modelcore/config/spec.py this path builds)
+# -----------------------------------------------------------------------------------------------
+@dataclass
+class ComponentSpec:
+    type: str
+    params: dict = field(default_factory=dict)
+
+    @staticmethod
+    def from_dict(d):
+        if isinstance(d, ComponentSpec):
+            return d
+        params = {}
+        for key, value in d.items():
+            if key == TYPE_KEY or key.startswith("//"):
+                continue
+            params[key] = _spec_tree(value)
+        return ComponentSpec(d[TYPE_KEY], params)
+
+
+def _spec_tree(value):
+    if isinstance(value, dict) and TYPE_KEY in value:
+        return ComponentSpec.from_dict(value)
+    if isinstance(value, list):
+        return [_spec_tree(v) for v in value]
+    return value
+
+
+@dataclass
+class ModelConfig:
+    sequence_len: int
+    vocab_size: int
+    n_embd: int
+    pad_vocab_size_to: int = 64
+    template: str = "base"
+    shared: dict = field(default_factory=dict)
+    input: ComponentSpec | None = None
+    body: ComponentSpec | None = None
+    output: ComponentSpec | None = None
+
+    @property
+    def padded_vocab_size(self):
+        m = self.pad_vocab_size_to
+        return ((self.vocab_size + m - 1) // m) * m
+
+    @staticmethod
+    def from_dict(d):
+        """A v3 config dict (``"#type"`` keys) -> ModelConfig."""
+        return ModelConfig(
+            sequence_len=d["sequence_len"], vocab_size=d["vocab_size"], n_embd=d["n_embd"],
+            pad_vocab_size_to=d.get("pad_vocab_size_to", 64), template=d.get("template", "base"),
+            shared={k: ComponentSpec.from_dict(v) for k, v in d.get("shared", {}).items()},
+            input=ComponentSpec.from_dict(d["input"]), body=ComponentSpec.from_dict(d["body"]),
+            output=ComponentSpec.from_dict(d["output"]))
+
+
+@dataclass
+class AttentionLayerSpec:
+    """What a KV cache needs from one attention layer (modelcore/config/spec.py:41-56)."""
+    n_head: int
+    n_kv_head: int
+    head_dim: int
+    window: int
+    kv_slot: int
+
+
+# -----------------------------------------------------------------------------------------------
+# Components
+# -----------------------------------------------------------------------------------------------
+class Linear(nn.Linear):
+    """fp32 master weight, cast to the activation dtype at every call."""
+
+    def forward(self, x):
+        return F.linear(x, self.weight.to(dtype=x.dtype))
+
+
+class RMSNorm(nn.Module):
+    """Parameterless RMSNorm over the last dim; eps=None is torch's default (the dtype's epsilon)."""
+
+    def __init__(self, eps=None):
+        super().__init__()
+        self.eps = eps
+
+    def init_weights(self):
+        pass
+
+    def forward(self, x):
+        return F.rms_norm(x, (x.size(-1),), eps=self.eps)
+
+
+def rope_tables(n_pos, head_dim, device, dtype, base=100000):
+    """cos/sin of the half-split rotation, (1, n_pos, 1, head_dim/2), computed in fp32 then cast
+    (modelcore/components/rope.py:15-27)."""
+    inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32, device=device)
+                                / head_dim))
+    angles = torch.outer(torch.arange(n_pos, dtype=torch.float32, device=device), inv_freq)
+    return (angles.cos().to(dtype)[None, :, None, :], angles.sin().to(dtype)[None, :, None, :])
+
+
+def rotate(x, cos, sin):
+    """Rotation of (first half, second half) of the last dim by -theta
+    (modelcore/components/rope.py:4-12)."""
+    half = x.shape[3] // 2
+    a, b = x[..., :half], x[..., half:]
+    return torch.cat([a * cos + b * sin, a * (-sin) + b * cos], 3)
+
+
+class Rotary(nn.Module):
+    """Owns the cos/sin tables (sequence_len * over_compute positions) and finds each query's
+    position from the cache: the shared position when the cache is uniform, a per-row gather of
+    cache_seqlens when it is right-ragged (modelcore/components/rotary.py:43-67)."""
+
+    def __init__(self, head_dim, sequence_len, over_compute, runtime):
+        super().__init__()
+        self.head_dim = head_dim
+        self.runtime = runtime
+        self.n_pos = sequence_len * over_compute
+        cos, sin = rope_tables(self.n_pos, head_dim, torch.empty(0).device, runtime.compute_dtype)
+        self.register_buffer("cos", cos, persistent=False)
+        self.register_buffer("sin", sin, persistent=False)
+
+    @torch.no_grad()
+    def init_weights(self):
+        self.cos, self.sin = rope_tables(self.n_pos, self.head_dim, self.cos.device,
+                                         self.runtime.compute_dtype)
+
+    def _cos_sin(self, T, kv_cache):
+        pos = 0 if kv_cache is None else kv_cache.uniform_pos()
+        if pos is not None:
+            assert pos + T <= self.cos.size(1), \
+                f"Sequence length grew beyond the rotary embeddings cache: {pos + T} > {self.cos.size(1)}"
+            return self.cos[:, pos:pos + T], self.sin[:, pos:pos + T]
+        idx = kv_cache.cache_seqlens.to(torch.long)[:, None] + torch.arange(
+            T, device=kv_cache.cache_seqlens.device)
+        # One host read, as in the reference: an index past the table must fail here, not in the
+        # gather kernel.
+        assert int(idx.max().item()) < self.cos.size(1), \
+            f"Sequence length grew beyond the rotary embeddings cache: {int(idx.max().item()) + 1} > {self.cos.size(1)}"
+        B = idx.size(0)
+        flat = idx.reshape(-1)
+        return (self.cos[0].index_select(0, flat).view(B, T, 1, -1),
+                self.sin[0].index_select(0, flat).view(B, T, 1, -1))
+
+    def forward(self, q, k, kv_cache):
+        cos, sin = self._cos_sin(q.size(1), kv_cache)
+        return rotate(q, cos, sin), rotate(k, cos, sin)
+
+    def apply_to_q(self, q, kv_cache):
+        cos, sin = self._cos_sin(q.size(1), kv_cache)
+        return rotate(q, cos, sin)
+
+
+class OutputGate(nn.Module):
+    """y * sigmoid(W . x[..., :in_channels]) per head, per element or per block of outputs, between
+    the attention operator and c_proj (modelcore/components/features.py:46-88)."""
+
+    def __init__(self, n_embd, n_head, head_dim, granularity, block_size=None, in_channels=None):
+        super().__init__()
+        self.in_channels = n_embd if in_channels is None else in_channels
+        if granularity == "head":
+            self.gates_per_head = 1
+        elif granularity == "element":
+            self.gates_per_head = head_dim
+        elif granularity == "block":
+            assert head_dim % block_size == 0, \
+                f"head_dim ({head_dim}) must be divisible by block_size ({block_size})"
+            self.gates_per_head = head_dim // block_size
+        else:
+            raise ValueError(f"unknown output_gate granularity {granularity!r}")
+        self.proj = Linear(self.in_channels, n_head * self.gates_per_head, bias=False)
+
+    @torch.no_grad()
+    def init_weights(self):
+        s = 3 ** 0.5 * self.in_channels ** -0.5
+        nn.init.uniform_(self.proj.weight, -s, s)
+
+    def forward(self, y, x):
+        B, T, H, D = y.shape
+        G = self.gates_per_head
+        gate = torch.sigmoid(self.proj(x[..., :self.in_channels])).view(B, T, H, G, 1)
+        return (y.reshape(B, T, H, G, D // G) * gate).view(B, T, H, D)
+
+
+class Attention(nn.Module):
+    """GQA attention with RoPE, QK-norm and x1.2 on q and k, calling the cached-attention operator
+    (modelcore/components/attention.py:53-184). A layer with produces_kv=False has no c_k/c_v and
+    reads the producer's already rotated/normed/scaled K/V from the per-forward kv_bus; it still
+    passes them to the operator, which rewrites identical values at the same positions."""
+
+    def __init__(self, n_embd, n_head, n_kv_head, head_dim, window, kv_slot, produces_kv,
+                 features, rope, norm, attention):
+        super().__init__()
+        if head_dim is None:
+            assert n_embd % n_head == 0
+            head_dim = n_embd // n_head
+        assert n_kv_head <= n_head and n_head % n_kv_head == 0
+        if not produces_kv and kv_slot is None:
+            raise ValueError("produces_kv=False requires an explicit kv_slot")
+        self.n_embd, self.n_head, self.n_kv_head, self.head_dim = n_embd, n_head, n_kv_head, head_dim
+        self.window = window
+        self._kv_slot = kv_slot
+        self.kv_slot = kv_slot
+        self.produces_kv = produces_kv
+        self.rope, self.norm, self.attention = rope, norm, attention
+        self.c_q = Linear(n_embd, n_head * head_dim, bias=False)
+        self.c_k = Linear(n_embd, n_kv_head * head_dim, bias=False) if produces_kv else None
+        self.c_v = Linear(n_embd, n_kv_head * head_dim, bias=False) if produces_kv else None
+        self.c_proj = Linear(n_head * head_dim, n_embd, bias=False)
+        self.features = nn.ModuleDict()
+        for spec in features or []:
+            if spec.type != "output_gate":
+                raise NotImplementedError(f"attention feature {spec.type!r} is not supported")
+            self.features["output_gate"] = OutputGate(n_embd, n_head, head_dim, **spec.params)
+
+    def bind_layer(self, layer_idx):
+        self.layer_idx = layer_idx
+        self.kv_slot = layer_idx if self._kv_slot is None else self._kv_slot
+
+    @torch.no_grad()
+    def init_weights(self):
+        s = 3 ** 0.5 * self.n_embd ** -0.5
+        nn.init.uniform_(self.c_q.weight, -s, s)
+        if self.produces_kv:
+            nn.init.uniform_(self.c_k.weight, -s, s)
+            nn.init.uniform_(self.c_v.weight, -s, s)
+        nn.init.zeros_(self.c_proj.weight)
+        for f in self.features.values():
+            f.init_weights()
+
+    def layer_spec(self):
+        return AttentionLayerSpec(self.n_head, self.n_kv_head, self.head_dim, self.window,
+                                  self.kv_slot)
+
+    def forward(self, x, kv_cache, kv_bus):
+        B, T, _ = x.size()
+        q = self.c_q(x).view(B, T, self.n_head, self.head_dim)
+        if self.produces_kv:
+            k = self.c_k(x).view(B, T, self.n_kv_head, self.head_dim)
+            v = self.c_v(x).view(B, T, self.n_kv_head, self.head_dim)
+            q, k = self.rope(q, k, kv_cache)
+            q, k = self.norm(q), self.norm(k)
+            q, k = q * 1.2, k * 1.2
+            kv_bus[self.kv_slot] = (k, v)
+        else:
+            k, v = kv_bus[self.kv_slot]
+            q = self.norm(self.rope.apply_to_q(q, kv_cache)) * 1.2
+        window_size = (self.window, 0)
+        if kv_cache is None:
+            y = self.attention.flash_attn_func(q, k, v, causal=True, window_size=window_size)
+        else:
+            k_cache, v_cache = kv_cache.get_slot_cache(self.kv_slot)
+            y = self.attention.flash_attn_with_kvcache(q, k_cache, v_cache, k=k, v=v,
+                                                       cache_seqlens=kv_cache.cache_seqlens,
+                                                       causal=True, window_size=window_size)
+        if "output_gate" in self.features:
+            y = self.features["output_gate"](y, x)
+        return self.c_proj(y.contiguous().view(B, T, -1))
+
+
+_ACTIVATIONS = {"silu": F.silu, "gelu": F.gelu, "relu": F.relu,
+                "relu2": lambda x: F.relu(x).square()}
+
+
+class GatedMLP(nn.Module):
+    """down(act(gate(x)) * up(x)) (modelcore/components/mlp.py:64-90)."""
+
+    def __init__(self, n_embd, activation, hidden_dim):
+        super().__init__()
+        self.n_embd = n_embd
+        self.act = _ACTIVATIONS[activation]
+        self.gate_proj = Linear(n_embd, hidden_dim, bias=False)
+        self.up_proj = Linear(n_embd, hidden_dim, bias=False)
+        self.down_proj = Linear(hidden_dim, n_embd, bias=False)
+
+    @torch.no_grad()
+    def init_weights(self):
+        s = 3 ** 0.5 * self.n_embd ** -0.5
+        nn.init.uniform_(self.gate_proj.weight, -s, s)
+        nn.init.uniform_(self.up_proj.weight, -s, s)
+        nn.init.zeros_(self.down_proj.weight)
+
+    def forward(self, x):
+        return self.down_proj(self.act(self.gate_proj(x)) * self.up_proj(x))
+
+
+class MLP(nn.Module):
+    """c_proj(act(c_fc(x))) (modelcore/components/mlp.py:37-61)."""
+
+    def __init__(self, n_embd, activation, hidden_dim):
+        super().__init__()
+        self.n_embd = n_embd
+        self.act = _ACTIVATIONS[activation]
+        self.c_fc = Linear(n_embd, hidden_dim, bias=False)
+        self.c_proj = Linear(hidden_dim, n_embd, bias=False)
+
+    @torch.no_grad()
+    def init_weights(self):
+        s = 3 ** 0.5 * self.n_embd ** -0.5
+        nn.init.uniform_(self.c_fc.weight, -s * 0.4, s * 0.4)
+        nn.init.zeros_(self.c_proj.weight)
+
+    def forward(self, x):
+        return self.c_proj(self.act(self.c_fc(x)))
+
+
+class Block(nn.Module):
+    """x + mixer(norm(x)), then x + ffn(norm(x)) (modelcore/components/block.py:54-60)."""
+
+    def __init__(self, layer_idx, mixer, ffn, norm):
+        super().__init__()
+        self.layer_idx = layer_idx
+        self.mixer = mixer
+        self.mixer.bind_layer(layer_idx)
+        self.ffn = ffn
+        self.norm = norm
+
+    @torch.no_grad()
+    def init_weights(self):
+        self.mixer.init_weights()
+        self.ffn.init_weights()
+
+    def forward(self, x, kv_cache, kv_bus):
+        x = x + self.mixer(self.norm(x), kv_cache, kv_bus)
+        return x + self.ffn(self.norm(x))
+
+
+class Stack(nn.Module):
+    """The layer loop; one fresh kv_bus per forward (modelcore/composers/stack.py:35-42)."""
+
+    def __init__(self, blocks):
+        super().__init__()
+        self.blocks = nn.ModuleList(blocks)
+
+    @torch.no_grad()
+    def init_weights(self):
+        for block in self.blocks:
+            block.init_weights()
+
+    def forward(self, x, kv_cache):
+        kv_bus = {}
+        for block in self.blocks:
+            x = block(x, kv_cache, kv_bus)
+        return x
+
+
+class TokenEmbedding(nn.Module):
+    """wte lookup, cast to the compute dtype, norm (modelcore/components/embedding.py:51-79)."""
+
+    def __init__(self, padded_vocab_size, n_embd, norm, runtime, smear=False):
+        super().__init__()
+        if smear:
+            raise NotImplementedError("token_embedding smear is not supported")
+        self.runtime = runtime
+        self.norm = norm
+        self.wte = nn.Embedding(padded_vocab_size, n_embd)
+
+    @torch.no_grad()
+    def init_weights(self):
+        nn.init.normal_(self.wte.weight, mean=0.0, std=0.8)
+        self.wte.to(dtype=self.runtime.compute_dtype)
+
+    def forward(self, idx):
+        return self.norm(self.wte(idx).to(self.runtime.compute_dtype))
+
+
+class LMHead(nn.Module):
+    """norm, projection, vocab crop, fp32, softcap * tanh(x / softcap)
+    (modelcore/components/unembedding.py:50-61)."""
+
+    def __init__(self, n_embd, vocab_size, padded_vocab_size, norm, softcap=None):
+        super().__init__()
+        self.vocab_size = vocab_size
+        self.norm = norm
+        self.softcap = softcap
+        self.lm_head = Linear(n_embd, padded_vocab_size, bias=False)
+
+    @torch.no_grad()
+    def init_weights(self):
+        nn.init.normal_(self.lm_head.weight, mean=0.0, std=0.001)
+
+    def forward(self, x):
+        logits = self.lm_head(self.norm(x))[..., :self.vocab_size].float()
+        if self.softcap is not None:
+            logits = self.softcap * torch.tanh(logits / self.softcap)
+        return logits
+
+
+# -----------------------------------------------------------------------------------------------
+# Model
+# -----------------------------------------------------------------------------------------------
+def _default_attention():
+    from modelcore_amd.kernels.flash_attn import flash_attn
+    return flash_attn
+
+
+class Model(nn.Module):
+    """Embedding -> blocks -> lm_head; advances the cache once per forward, after every layer
+    (modelcore/model.py:93-101)."""
+
+    def __init__(self, config: ModelConfig, runtime: Runtime | None = None, attention=None):
+        super().__init__()
+        self.config = config
+        self.runtime = runtime or Runtime()
+        attention = attention or _default_attention()
+        shared = {}
+        for name, spec in config.shared.items():
+            if spec.type == "rotary":
+                shared[name] = Rotary(spec.params["head_dim"], config.sequence_len,
+                                      spec.params.get("over_compute", 10), self.runtime)
+            elif spec.type == "rms_norm":
+                shared[name] = RMSNorm(spec.params.get("eps"))
+            else:
+                raise NotImplementedError(f"shared component {spec.type!r} is not supported")
+        self.shared = nn.ModuleDict(shared)
+        rope, norm = shared["rope"], shared["norm"]
+
+        inp = config.input
+        assert inp.type == "token_embedding", inp.type
+        self.embedding = TokenEmbedding(config.padded_vocab_size, config.n_embd, norm,
+                                        self.runtime, smear=inp.params.get("smear", False))
+        body = config.body
+        assert body.type == "stack", body.type
+        if body.params.get("features"):
+            raise NotImplementedError("stack features are not supported")
+        blocks = []
+        for spec in body.params["blocks"]:
+            assert spec.type == "block", spec.type
+            p = spec.params
+            if p.get("features"):
+                raise NotImplementedError("block features are not supported")
+            m = p["mixer"]
+            assert m.type == "attention", f"mixer {m.type!r} is not supported"
+            mp = m.params
+            mixer = Attention(config.n_embd, mp["n_head"], mp.get("n_kv_head", mp["n_head"]),
+                              mp.get("head_dim"), mp.get("window", -1), mp.get("kv_slot"),
+                              mp.get("produces_kv", True), mp.get("features"), rope, norm,
+                              attention)
+            f = p["ffn"]
+            ffn_cls = {"gated_mlp": GatedMLP, "mlp": MLP}[f.type]
+            ffn = ffn_cls(config.n_embd, f.params["activation"], f.params["hidden_dim"])
+            blocks.append(Block(p["layer_idx"], mixer, ffn, norm))
+        self.body = Stack(blocks)
+        out = config.output
+        assert out.type == "lm_head", out.type
+        self.unembedding = LMHead(config.n_embd, config.vocab_size, config.padded_vocab_size, norm,
+                                  out.params.get("softcap"))
+
+    @torch.no_grad()
+    def init_weights(self):
+        """RNG draws in the reference's order: embedding, shared, blocks in order (attention then
+        ffn), lm_head (modelcore/model.py:63-69)."""
+        self.embedding.init_weights()
+        for m in self.shared.values():
+            m.init_weights()
+        self.body.init_weights()
+        self.unembedding.init_weights()
+
+    def layer_specs(self):
+        return [b.mixer.layer_spec() for b in self.body.blocks]
+
+    def get_device(self):
+        return next(self.parameters()).device
+
+    def forward(self, idx, targets=None, kv_cache=None):
+        if targets is not None:
+            raise NotImplementedError("training loss is not part of the inference path")
+        x = self.embedding(idx)
+        x = self.body(x, kv_cache)
+        if kv_cache is not None:
+            kv_cache.advance(idx.size(1))
+        return self.unembedding(x)
+
+
+def kv_cache_spec(layer_specs):
+    """num_kv_slots / n_kv_head / head_dim for KVCache (modelcore/stats.py:110-131): one slot per
+    distinct kv_slot, which must form 0..M-1; uniform n_kv_head and head_dim."""
+    assert layer_specs, "layer_specs is empty"
+    assert len({s.n_kv_head for s in layer_specs}) == 1 and \
+        len({s.head_dim for s in layer_specs}) == 1, \
+        "kv_cache_spec() requires uniform n_kv_head/head_dim across layers"
+    slots = {s.kv_slot for s in layer_specs}
+    assert slots == set(range(len(slots))), \
+        "kv_cache_spec() requires kv slots to be a contiguous 0..M-1 range"
+    return {"n_kv_head": layer_specs[0].n_kv_head, "head_dim": layer_specs[0].head_dim,
+            "num_kv_slots": len(slots)}
+
+
+class ModelManager:
+    """create_model / new_kv_cache / new_decoder (modelcore/manager.py:111-119, :286-299)."""
+
+    def __init__(self, runtime: Runtime | None = None, attention=None):
+        self.runtime = runtime or Runtime()
+        self.attention = attention
+
+    def create_model(self, config, *, device, seed=None):
+        if isinstance(config, dict):
+            config = ModelConfig.from_dict(config)
+        with torch.device("meta"):
+            model = Model(config, runtime=self.runtime, attention=self.attention)
+        model.to_empty(device=device)
+        if seed is not None:
+            torch.manual_seed(seed)
+        model.init_weights()
+        return model
+
+    def new_kv_cache(self, model, *, batch_size, seq_len, device=None):
+        spec = kv_cache_spec(model.layer_specs())
+        return KVCache(batch_size=batch_size, seq_len=seq_len,
+                       device=device or model.get_device(), dtype=self.runtime.compute_dtype,
+                       **spec)
+
+    def new_decoder(self, model, tokens, *, num_samples=1, max_tokens=None, device=None):
+        from modelcore_amd.generate import Decoder
+        return Decoder(model, self, tokens, num_samples=num_samples, max_tokens=max_tokens,
+                       device=device)
+
+
+def param_count(model) -> int:
+    return sum(p.numel() for p in model.parameters())

@@ -6,9 +6,14 @@
   the furthest row; ``scaled_dot_product_attention`` with ``enable_gqa`` -- sliced and unmasked
   for a uniform single token (:217-224), causal for a uniform full prompt (:213-215), an explicit
   (Tq, Tk) mask for uniform chunks (:226-244), a (B, 1, T_new, Tk) mask when ragged (:246-264).
+* ``flash_attn_func`` follows the no-cache fallback (modelcore/kernels/flash_attn.py:270-303
+  without FA3 or document masks): transpose to (B, H, T, D), then the same uniform helper.
 * ``replicate`` follows KVCache.prefill's broadcast copy (modelcore/cache.py:84-85).
+* ``flash_attn`` is the operator namespace of the two functions, for model code that takes one.
 """
 from __future__ import annotations
+
+from types import SimpleNamespace
 
 import torch
 import torch.nn.functional as F
@@ -42,7 +47,7 @@ def _ragged_mask(cache_seqlens, T_new, Tk, window):
 
 
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
-                            window_size=(-1, -1), force_ragged=False):
+                            window_size=(-1, -1), force_ragged=False, causal=True):
     """CPU fallback of the operator: in-place append into k_cache/v_cache, returns (B, T_new, H, D)."""
     B, T_new, H, D = q.shape
     positions = cache_seqlens.tolist()
@@ -71,7 +76,28 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
     return y.transpose(1, 2)
 
 
+def flash_attn_func(q, k, v, causal=True, window_size=(-1, -1), doc_args=None):
+    """No-cache causal attention, (B, T, H, D) in and out."""
+    assert doc_args is None
+    qs, ks, vs = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    y = _uniform_attention(qs, ks, vs, window_size[0], qs.size(1) != ks.size(1))
+    return y.transpose(1, 2)
+
+
+flash_attn = SimpleNamespace(flash_attn_func=flash_attn_func,
+                             flash_attn_with_kvcache=flash_attn_with_kvcache)
+
+
 def replicate(dst_k, dst_v, src_k, src_v, n_tokens):
     """Broadcast row 0 of a (S, 1, T, H_kv, D) source into every row of (S, B, T', H_kv, D)."""
     dst_k[:, :, :n_tokens] = src_k[:, :, :n_tokens]
     dst_v[:, :, :n_tokens] = src_v[:, :, :n_tokens]
+
+
+def replicate_rows(dst, src, row_begin, n_rows, n_tokens):
+    """KVCache-level copy of row 0, positions [0, n_tokens), of every slot of `src` into rows
+    [row_begin, row_begin + n_rows) of `dst` (modelcore/cache.py:84-85 and :106-107); the same
+    argument meaning as modelcore_amd.cache.KVCache._replicate_from, for CPU caches."""
+    rows = slice(row_begin, row_begin + n_rows)
+    dst.k_cache[:, rows, :n_tokens] = src.k_cache[:, 0:1, :n_tokens]
+    dst.v_cache[:, rows, :n_tokens] = src.v_cache[:, 0:1, :n_tokens]

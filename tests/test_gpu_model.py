@@ -1,0 +1,162 @@
+"""The model harness on the GPU, attention through the HIP kernels, against the same model on the
+CPU with the oracle operator (tests/test_model_host.py pins that one) and against the reference's
+goldens.
+
+* Goldens (fp32, head_dim 16): no-cache logits, and a prefill plus cached single-token steps,
+  match the reference's logits to 1e-4.
+* The README quickstart model (12 layers, 768 wide, 12/12 heads of 64, gated SiLU MLP 2048, vocab
+  32768, softcap 15, fp32, seed-0 weights drawn on the CPU): batch 2, prompts of 16 tokens, 64
+  greedy tokens -- the token ids equal the CPU oracle's exactly, with the seed-0 weights (whose
+  zero-init projections make attention irrelevant) and with awake weights (where it is not).
+* A mixed-window, KV-sharing stack in bf16 (head_dim 128, GQA 12/4): logits of a prefill and of
+  cached decode steps stay within bf16 tolerance of the fp32 CPU oracle.
+"""
+import pytest
+import torch
+
+import _goldens
+from modelcore_amd.generate import sample_next_token
+from modelcore_amd.model import ComponentSpec, ModelConfig, ModelManager
+from modelcore_amd.runtime import Runtime
+from oracle import sdpa_fallback
+from test_model_host import awake
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+CPU = torch.device("cpu")
+
+
+def _note(*a):
+    print("case:", *a, flush=True)
+
+
+def gpu_manager(dtype=torch.float32):
+    return ModelManager(Runtime(dtype))
+
+
+def cpu_manager():
+    return ModelManager(Runtime(torch.float32), attention=sdpa_fallback.flash_attn)
+
+
+@pytest.fixture
+def cpu_cache_copies(monkeypatch):
+    from modelcore_amd.cache import KVCache
+    real = KVCache._replicate_from
+
+    def copy(self, other, r0, n, t):
+        if self.k_cache.device.type == "cpu":
+            return sdpa_fallback.replicate_rows(self, other, r0, n, t)
+        return real(self, other, r0, n, t)
+
+    monkeypatch.setattr(KVCache, "_replicate_from", copy)
+
+
+@pytest.mark.parametrize("name", _goldens.GOLDENS)
+def test_goldens_no_cache_and_cached_on_the_gpu(name):
+    _note("golden", name)
+    mgr = gpu_manager()
+    model, idx, logits = _goldens.build(name, mgr, DEV)
+    idx = idx.to(DEV)
+    with torch.no_grad():
+        full = model(idx).cpu()
+        torch.testing.assert_close(full, logits, atol=1e-4, rtol=0)
+        cache = mgr.new_kv_cache(model, batch_size=idx.size(0), seq_len=idx.size(1))
+        parts = [model(idx[:, :5], kv_cache=cache)]
+        for t in range(5, idx.size(1)):
+            parts.append(model(idx[:, t:t + 1], kv_cache=cache))
+    torch.testing.assert_close(torch.cat(parts, dim=1).cpu(), logits, atol=1e-4, rtol=0)
+
+
+def quickstart_config():
+    hd = 64
+    blocks = [ComponentSpec("block", {
+        "layer_idx": i, "features": [],
+        "mixer": ComponentSpec("attention", {"n_head": 12, "n_kv_head": 12, "head_dim": hd,
+                                             "window": -1, "kv_slot": None, "produces_kv": True,
+                                             "features": []}),
+        "ffn": ComponentSpec("gated_mlp", {"activation": "silu", "hidden_dim": 2048})})
+        for i in range(12)]
+    return ModelConfig(sequence_len=1024, vocab_size=32768, n_embd=768, pad_vocab_size_to=64,
+                       shared={"rope": ComponentSpec("rotary", {"head_dim": hd, "over_compute": 10}),
+                               "norm": ComponentSpec("rms_norm", {"eps": None})},
+                       input=ComponentSpec("token_embedding", {"smear": False}),
+                       body=ComponentSpec("stack", {"blocks": blocks, "features": []}),
+                       output=ComponentSpec("lm_head", {"softcap": 15}))
+
+
+def greedy_ids(mgr, model, prompts, n):
+    dec = mgr.new_decoder(model, prompts, num_samples=1, max_tokens=n)
+    rows = [[] for _ in prompts]
+    for _ in range(n):
+        nxt = sample_next_token(dec.logits, rng=None, temperature=0.0)
+        for r, t in enumerate(nxt.view(-1).tolist()):
+            rows[r].append(t)
+        dec.step(nxt.view(-1))
+    return rows
+
+
+@pytest.mark.parametrize("wake", [False, True], ids=["seed0", "awake"])
+def test_quickstart_greedy_ids_equal_the_cpu_oracle(wake, cpu_cache_copies):
+    _note("quickstart greedy", "awake" if wake else "seed0")
+    cfg = quickstart_config()
+    cpu_mgr = cpu_manager()
+    cpu_model = cpu_mgr.create_model(cfg, device=CPU, seed=0)
+    if wake:
+        awake(cpu_model)
+    gpu_mgr = gpu_manager()
+    gpu_model = gpu_mgr.create_model(cfg, device=DEV, seed=0)
+    gpu_model.load_state_dict(cpu_model.state_dict())
+    g = torch.Generator().manual_seed(0)
+    prompts = torch.randint(0, cfg.vocab_size, (2, 16), generator=g).tolist()
+    want = greedy_ids(cpu_mgr, cpu_model, prompts, 64)
+    got = greedy_ids(gpu_mgr, gpu_model, prompts, 64)
+    assert got == want
+
+
+def mixed_window_config(n_layer=8):
+    """Layer i is global iff i % 4 == 3, else window 64; odd layers read the previous layer's
+    slot."""
+    blocks = []
+    for i in range(n_layer):
+        consumer = i % 2 == 1
+        blocks.append(ComponentSpec("block", {
+            "layer_idx": i, "features": [],
+            "mixer": ComponentSpec("attention", {
+                "n_head": 12, "n_kv_head": 4, "head_dim": 128,
+                "window": -1 if i % 4 == 3 else 64, "kv_slot": (i - 1) // 2 if consumer else i // 2,
+                "produces_kv": not consumer, "features": []}),
+            "ffn": ComponentSpec("gated_mlp", {"activation": "silu", "hidden_dim": 768})}))
+    return ModelConfig(sequence_len=512, vocab_size=512, n_embd=384,
+                       shared={"rope": ComponentSpec("rotary", {"head_dim": 128,
+                                                                "over_compute": 10}),
+                               "norm": ComponentSpec("rms_norm", {"eps": None})},
+                       input=ComponentSpec("token_embedding", {"smear": False}),
+                       body=ComponentSpec("stack", {"blocks": blocks, "features": []}),
+                       output=ComponentSpec("lm_head", {"softcap": 15}))
+
+
+def test_mixed_window_kv_sharing_stack_in_bf16(cpu_cache_copies):
+    _note("mixed-window bf16 stack")
+    cfg = mixed_window_config()
+    cpu_mgr = cpu_manager()
+    cpu_model = awake(cpu_mgr.create_model(cfg, device=CPU, seed=0))
+    gpu_mgr = gpu_manager(torch.bfloat16)
+    gpu_model = gpu_mgr.create_model(cfg, device=DEV, seed=0)
+    gpu_model.load_state_dict(cpu_model.state_dict())
+    g = torch.Generator().manual_seed(1)
+    B, P, steps = 4, 200, 6
+    prompt = torch.randint(0, cfg.vocab_size, (B, P + steps), generator=g)
+    cpu_cache = cpu_mgr.new_kv_cache(cpu_model, batch_size=B, seq_len=P + steps)
+    gpu_cache = gpu_mgr.new_kv_cache(gpu_model, batch_size=B, seq_len=P + steps)
+    assert gpu_cache.n_slots == 4 and gpu_cache.k_cache.dtype == torch.bfloat16
+    with torch.no_grad():
+        want = [cpu_model(prompt[:, :P], kv_cache=cpu_cache)[:, -1]]
+        got = [gpu_model(prompt[:, :P].to(DEV), kv_cache=gpu_cache)[:, -1].cpu()]
+        for t in range(P, P + steps):
+            want.append(cpu_model(prompt[:, t:t + 1], kv_cache=cpu_cache)[:, -1])
+            got.append(gpu_model(prompt[:, t:t + 1].to(DEV), kv_cache=gpu_cache)[:, -1].cpu())
+    for i, (a, b) in enumerate(zip(got, want)):
+        err = (a - b).abs().max().item()
+        assert err <= 0.15, f"call {i}: logits max-abs {err}"
+    assert gpu_cache.cache_seqlens.tolist() == [P + steps] * B

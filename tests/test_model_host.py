@@ -1,0 +1,197 @@
+"""The model harness around the KV path, on the CPU with the oracle operator plugged in
+(``attention=oracle.sdpa_fallback.flash_attn``): this pins the harness's own arithmetic (embedding,
+RoPE, QK-norm, x1.2, KV sharing, output gate, MLP, softcap, cache bookkeeping) before the GPU
+tests run the same model on the HIP operator.
+
+* The reference's goldens (tests/golden/README.md): no-cache logits within 2e-6 of what the
+  reference produced (the reference asserts bit-identity on the machine that wrote them; here 85%
+  of the logits differ in the last one to four bits, the signature of a different CPU matmul
+  kernel, while a planted mistake moves them by 0.2 or more); a prefill followed by cached
+  single-token steps reproduces them to 1e-4.
+* Decoder at temperature 0 equals a naive no-cache greedy loop (modelcore/tests/test_generate.py:
+  49-67), on "awake" weights (zero-init projections given small random values, as at
+  test_generate.py:187-201), so attention actually affects the tokens.
+* Multi-prompt (right-ragged) decode equals each prompt decoded alone (test_generate.py:220-234).
+"""
+import pytest
+import torch
+
+import _goldens
+from modelcore_amd.generate import sample_next_token
+from modelcore_amd.model import ComponentSpec, ModelConfig, ModelManager, kv_cache_spec
+from modelcore_amd.runtime import Runtime
+from oracle import sdpa_fallback
+
+CPU = torch.device("cpu")
+
+
+@pytest.fixture(autouse=True)
+def cpu_cache_copies(monkeypatch):
+    """KVCache's row copies run the HIP replication kernel; on CPU caches the oracle's restated
+    copy stands in for it, so Decoder can be exercised here."""
+    from modelcore_amd.cache import KVCache
+    monkeypatch.setattr(KVCache, "_replicate_from",
+                        lambda self, other, r0, n, t: sdpa_fallback.replicate_rows(self, other, r0, n, t))
+
+
+def manager():
+    return ModelManager(Runtime(torch.float32), attention=sdpa_fallback.flash_attn)
+
+
+GOLDEN_ATOL = 2e-6
+
+
+@pytest.mark.parametrize("name", _goldens.GOLDENS)
+def test_no_cache_logits_equal_the_reference_goldens(name):
+    model, idx, logits = _goldens.build(name, manager(), CPU)
+    with torch.no_grad():
+        torch.testing.assert_close(model(idx), logits, atol=GOLDEN_ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("plant", ["rope_sign", "no_qk_scale", "window_plus_one", "gqa_roll"])
+def test_planted_harness_mistakes_miss_the_golden(plant, monkeypatch):
+    """Each plausible slip in the harness moves the golden logits far beyond the tolerance."""
+    import modelcore_amd.model as M
+    name = "v2_llama_kvshare_win_gated_block.pt"
+    if plant == "rope_sign":
+        rot = M.rotate
+        monkeypatch.setattr(M, "rotate", lambda x, c, s: rot(x, c, -s))
+    model, idx, logits = _goldens.build(name, manager(), CPU)
+    for blk in model.body.blocks:
+        if plant == "window_plus_one":
+            blk.mixer.window += 1
+        if plant == "no_qk_scale":
+            blk.mixer.norm = M.RMSNorm(None)
+            blk.mixer.norm.forward = lambda x: M.F.rms_norm(x, (x.size(-1),)) / 1.2
+        if plant == "gqa_roll" and blk.mixer.produces_kv:
+            w = blk.mixer.c_k.weight
+            w.data = w.data.view(2, 16, -1).flip(0).reshape_as(w)
+    with torch.no_grad():
+        assert (model(idx) - logits).abs().max() > 1e-2
+
+
+@pytest.mark.parametrize("name", _goldens.GOLDENS)
+def test_prefill_then_cached_steps_reproduce_the_golden_logits(name):
+    """A 4-token prefill into the cache, then one cached step per remaining token."""
+    mgr = manager()
+    model, idx, logits = _goldens.build(name, mgr, CPU)
+    B, T = idx.shape
+    cache = mgr.new_kv_cache(model, batch_size=B, seq_len=T)
+    with torch.no_grad():
+        parts = [model(idx[:, :4], kv_cache=cache)]
+        for t in range(4, T):
+            parts.append(model(idx[:, t:t + 1], kv_cache=cache))
+    assert cache.get_pos() == T
+    torch.testing.assert_close(torch.cat(parts, dim=1), logits, atol=1e-4, rtol=0)
+
+
+def tiny_config(window=8, kv_share=False, gate=False, n_layer=4):
+    blocks = []
+    for i in range(n_layer):
+        consumer = kv_share and i % 2 == 1
+        mixer = ComponentSpec("attention", {
+            "n_head": 4, "n_kv_head": 2, "head_dim": 16, "window": window if i % 4 != 3 else -1,
+            "kv_slot": (i - 1) // 2 if consumer else (i // 2 if kv_share else None),
+            "produces_kv": not consumer,
+            "features": [ComponentSpec("output_gate", {"granularity": "head", "block_size": None,
+                                                       "in_channels": None})] if gate else []})
+        blocks.append(ComponentSpec("block", {"layer_idx": i, "features": [], "mixer": mixer,
+                                              "ffn": ComponentSpec("gated_mlp", {
+                                                  "activation": "silu", "hidden_dim": 96})}))
+    return ModelConfig(sequence_len=64, vocab_size=100, n_embd=48,
+                       shared={"rope": ComponentSpec("rotary", {"head_dim": 16, "over_compute": 10}),
+                               "norm": ComponentSpec("rms_norm", {"eps": None})},
+                       input=ComponentSpec("token_embedding", {"smear": False}),
+                       body=ComponentSpec("stack", {"blocks": blocks, "features": []}),
+                       output=ComponentSpec("lm_head", {"softcap": 15}))
+
+
+def awake(model, seed=0):
+    """Give every all-zero parameter small random values (test_generate.py:187-201)."""
+    g = torch.Generator().manual_seed(seed + 1)
+    with torch.no_grad():
+        for p in model.parameters():
+            if p.numel() and p.abs().sum() == 0:
+                p.copy_((torch.randn(p.shape, generator=g) * 0.1).to(p.dtype))
+    return model
+
+
+def naive_greedy(model, tokens, n):
+    ids = torch.tensor([tokens], dtype=torch.long)
+    out = []
+    with torch.no_grad():
+        for _ in range(n):
+            nxt = sample_next_token(model(ids)[:, -1, :], rng=None, temperature=0.0)
+            ids = torch.cat((ids, nxt), dim=1)
+            out.append(nxt.item())
+    return out
+
+
+def cached_greedy(mgr, model, tokens, n):
+    dec = mgr.new_decoder(model, tokens, num_samples=1, max_tokens=n)
+    out = []
+    for _ in range(n):
+        tok = sample_next_token(dec.logits, rng=None, temperature=0.0).item()
+        out.append(tok)
+        dec.step([tok])
+    return out
+
+
+@pytest.mark.parametrize("kv_share,gate", [(False, False), (True, False), (True, True)])
+def test_decoder_matches_naive_greedy_on_awake_weights(kv_share, gate):
+    mgr = manager()
+    model = awake(mgr.create_model(tiny_config(kv_share=kv_share, gate=gate), device=CPU, seed=0))
+    prompt = [5, 17, 3, 99, 42, 8, 61, 2, 13, 77]
+    assert cached_greedy(mgr, model, prompt, 12) == naive_greedy(model, prompt, 12)
+
+
+def test_multi_prompt_decode_matches_each_prompt_alone():
+    mgr = manager()
+    model = awake(mgr.create_model(tiny_config(kv_share=True), device=CPU, seed=0))
+    prompts = [[1, 2], [3, 4, 5, 6, 7], [8, 9, 10, 11, 12, 13, 14, 15, 16],
+               [2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13]]
+    dec = mgr.new_decoder(model, prompts, num_samples=2, max_tokens=10)
+    assert dec.kv_cache.uniform_pos() is None
+    rows = [[] for _ in range(len(prompts) * 2)]
+    for _ in range(10):
+        nxt = sample_next_token(dec.logits, rng=None, temperature=0.0)
+        for r, t in enumerate(nxt.view(-1).tolist()):
+            rows[r].append(t)
+        dec.step(nxt.view(-1))
+    for p, prompt in enumerate(prompts):
+        alone = cached_greedy(mgr, model, prompt, 10)
+        assert rows[2 * p] == alone and rows[2 * p + 1] == alone, f"prompt {p}"
+
+
+def test_kv_cache_spec_counts_distinct_slots():
+    mgr = manager()
+    model = mgr.create_model(tiny_config(kv_share=True, n_layer=6), device=CPU, seed=0)
+    assert [s.kv_slot for s in model.layer_specs()] == [0, 0, 1, 1, 2, 2]
+    assert kv_cache_spec(model.layer_specs()) == {"n_kv_head": 2, "head_dim": 16,
+                                                  "num_kv_slots": 3}
+    cache = mgr.new_kv_cache(model, batch_size=3, seq_len=20)
+    assert cache.k_cache.shape == (3, 3, 20, 2, 16) and cache.k_cache.dtype == torch.float32
+
+
+def test_seed_zero_init_follows_the_reference_scheme():
+    """Init distributions of modelcore/components/*.py: wte N(0, 0.8), q/k/v U(+-sqrt(3/n_embd)),
+    c_proj and down_proj zero, lm_head N(0, 0.001); same seed, same weights."""
+    mgr = manager()
+    a = mgr.create_model(tiny_config(), device=CPU, seed=0)
+    b = mgr.create_model(tiny_config(), device=CPU, seed=0)
+    for (ka, va), (kb, vb) in zip(a.state_dict().items(), b.state_dict().items()):
+        assert ka == kb and torch.equal(va, vb)
+    blk = a.body.blocks[0]
+    bound = 3 ** 0.5 * 48 ** -0.5
+    assert blk.mixer.c_q.weight.abs().max() <= bound and blk.mixer.c_q.weight.std() > bound / 3
+    assert not blk.mixer.c_proj.weight.any() and not blk.ffn.down_proj.weight.any()
+    assert abs(float(a.embedding.wte.weight.std()) - 0.8) < 0.05
+    assert abs(float(a.unembedding.lm_head.weight.std()) - 0.001) < 2e-4
+
+
+def test_the_default_operator_refuses_cpu_tensors():
+    """Without an injected operator the model runs the HIP kernels only: CPU tensors raise."""
+    mgr = ModelManager(Runtime(torch.float32))
+    model = mgr.create_model(tiny_config(), device=CPU, seed=0)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        model(torch.tensor([[1, 2, 3]]))
