@@ -32,8 +32,8 @@
 //    v_perm_b32, so each v_dot2_f32_bf16 adds two tokens' contributions to one output dim.
 //  * Output: a segment that covers its whole unit writes the normalised output; otherwise it
 //    writes (o, m, l) for its 16 heads to workspace slot wave + unit (distinct per segment, since
-//    units advance with the waves), and the merge pass combines a unit's segments by
-//    log-sum-exp.
+//    units advance with the waves), and the merge pass -- one wave per (unit, query head), lane
+//    l owning dims 2l and 2l + 1 -- combines a unit's segments by log-sum-exp.
 //  * Append: the segment that ends at p reads the new token from k/v instead of the cache and
 //    its lanes store it into the cache at p (bit-exact copy; the first query-head group only).
 #include "kernels.h"
@@ -197,62 +197,6 @@ struct WaveAcc {
   float l[KG][GM];
 };
 
-__device__ __forceinline__ void write_bf16x8(uint16_t *at, const float (&v)[8], float denom) {
-  const float inv = 1.f / denom;
-  uint4 v4;
-  v4.x = pack_bf16(v[0] * inv, v[1] * inv);
-  v4.y = pack_bf16(v[2] * inv, v[3] * inv);
-  v4.z = pack_bf16(v[4] * inv, v[5] * inv);
-  v4.w = pack_bf16(v[6] * inv, v[7] * inv);
-  *reinterpret_cast<uint4 *>(at) = v4;
-}
-
-// Merge of the nseg partials of unit ug (slots g_first + ug ...) by log-sum-exp, run by a
-// whole workgroup: wave wv takes KV-head row wv, lane (h, c) = (lane / 16, lane % 16) head h and
-// dims c*8..c*8+7. Up to 16 segments' loads are in flight at once.
-__device__ void merge_unit(const FusedParams &P, int ug, int g_first, int nseg) {
-  const int lane = threadIdx.x & 63;
-  const int mr = threadIdx.x >> 6;
-  const int mh = lane >> 4;
-  const int c = lane & 15;
-  const int b = ug / P.n_units;
-  const int unit = ug - b * P.n_units;
-  const int kg = unit / P.n_hc;
-  const int hc = unit - kg * P.n_hc;
-  const int kvh = kg * KG + mr;
-  const float *base = P.part + int64_t(g_first + ug) * kPart;
-  float MM = -INFINITY, LL = 0.f, tot[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) tot[e] = 0.f;
-  for (int s0 = 0; s0 < nseg; s0 += 16) {
-    float2 ml[16];
-    float2 v[16][4];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const float *ps = base + int64_t(s0 + min(k, nseg - 1 - s0)) * kPart;
-      ml[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * (mr * GM + mh));
-      const float *pv = ps + (mr * GM + mh) * D + c * 8;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[k][e] = *reinterpret_cast<const float2 *>(pv + 2 * e);
-    }
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      // Segments past nseg re-read the last one; they get weight 0 (m = -inf).
-      const float mk = s0 + k < nseg ? ml[k].x : -INFINITY;
-      const float m_new = fmaxf(MM, mk);
-      const float fa = exp2_or_zero(MM - m_new), fb = exp2_or_zero(mk - m_new);
-      LL = LL * fa + ml[k].y * fb;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        tot[2 * e] = tot[2 * e] * fa + v[k][e].x * fb;
-        tot[2 * e + 1] = tot[2 * e + 1] * fa + v[k][e].y * fb;
-      }
-      MM = m_new;
-    }
-  }
-  if (kvh < P.H_kv && mh < min(GM, P.G - hc * GM))
-    write_bf16x8(P.out + (int64_t(b) * P.H + int64_t(kvh) * P.G + hc * GM + mh) * D + c * 8, tot, LL);
-}
 
 // This workgroup's share of the slots: total T, active workgroups NG = min(n_groups, T), the
 // range [start, end), and the row b holding `start` with Pb its first slot. One read of
@@ -562,22 +506,51 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
   }
 }
 
-// Merge pass: one workgroup per unit; wave wv takes KV-head row wv of the unit. A unit split over
-// several workgroups of the streaming pass is combined from their partials by log-sum-exp.
-__global__ __launch_bounds__(256) void decode_merge_kernel(FusedParams P) {
-  const int lane = threadIdx.x & 63;
-  const int ug = blockIdx.x;
+// Merge pass with one wave per (unit, query head): lane l combines dims 2l, 2l+1 of that head
+// over the unit's segments, eight segments' loads in flight at a time.
+__global__ __launch_bounds__(64) void decode_merge_kernel(FusedParams P) {
+  const int lane = threadIdx.x;
+  const int ug = blockIdx.x / (KG * GM);
+  const int hr = blockIdx.x - ug * (KG * GM);  // KV row * GM + head within the unit
   const int b = ug / P.n_units;
   const int unit = ug - b * P.n_units;
+  const int kg = unit / P.n_hc;
+  const int hc = unit - kg * P.n_hc;
+  const int kvh = kg * KG + hr / GM;
+  const int hh = hr % GM;
+  if (kvh >= P.H_kv || hh >= min(GM, P.G - hc * GM)) return;
   int64_t T, Pb;
   int NG, lo;
   const int nk = row_geometry(P, b, lane, T, NG, Pb, lo);
   if (nk == 0) return;
   const int64_t unit_start = Pb + int64_t(unit) * nk;
   const int g_first = group_of(unit_start, T, NG);
-  const int g_last = group_of(unit_start + nk - 1, T, NG);
-  if (g_first == g_last) return;  // written directly by the streaming pass
-  merge_unit(P, ug, g_first, g_last - g_first + 1);
+  const int nseg = group_of(unit_start + nk - 1, T, NG) - g_first + 1;
+  if (nseg == 1) return;  // written directly by the streaming pass
+  const float *base = P.part + int64_t(g_first + ug) * kPart;
+  float M = -INFINITY, L = 0.f, t0 = 0.f, t1 = 0.f;
+  for (int s0 = 0; s0 < nseg; s0 += 8) {
+    float2 ml[8], v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float *ps = base + int64_t(min(s0 + k, nseg - 1)) * kPart;
+      ml[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * hr);
+      v[k] = *reinterpret_cast<const float2 *>(ps + hr * D + 2 * lane);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float mk = s0 + k < nseg ? ml[k].x : -INFINITY;
+      const float m_new = fmaxf(M, mk);
+      const float fa = exp2_or_zero(M - m_new), fb = exp2_or_zero(mk - m_new);
+      L = L * fa + ml[k].y * fb;
+      t0 = t0 * fa + v[k].x * fb;
+      t1 = t1 * fa + v[k].y * fb;
+      M = m_new;
+    }
+  }
+  const float inv = 1.f / L;
+  *reinterpret_cast<uint32_t *>(P.out + (int64_t(b) * P.H + int64_t(kvh) * P.G + hc * GM + hh) * D +
+                                2 * lane) = pack_bf16(t0 * inv, t1 * inv);
 }
 
 // Number of compute units of the current device (queried once per device).
@@ -644,8 +617,8 @@ int launch_decode_fused(const AttnArgs &a) {
   hipLaunchKernelGGL(decode_fused_kernel, dim3(unsigned(groups)), dim3(256), 0, a.stream, P);
   int st = launch_status("decode_fused");
   if (st != MCAMD_OK) return st;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(unsigned(a.batch * P.n_units)), dim3(256), 0,
-                     a.stream, P);
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(unsigned(a.batch * P.n_units * KG * GM)),
+                     dim3(64), 0, a.stream, P);
   return launch_status("decode_merge");
 }
 

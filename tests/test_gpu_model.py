@@ -158,5 +158,6 @@ def test_mixed_window_kv_sharing_stack_in_bf16(cpu_cache_copies):
             got.append(gpu_model(prompt[:, t:t + 1].to(DEV), kv_cache=gpu_cache)[:, -1].cpu())
     for i, (a, b) in enumerate(zip(got, want)):
         err = (a - b).abs().max().item()
+        print(f"call {i}: logits max-abs {err:.4f} (scale {b.abs().max().item():.3f})", flush=True)
         assert err <= 0.15, f"call {i}: logits max-abs {err}"
     assert gpu_cache.cache_seqlens.tolist() == [P + steps] * B
