@@ -42,9 +42,13 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
-    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "prefill", "replicate", "mixed"),
+                    default="decode",
                     help="decode: the decode microbench (default, the headline metric); prefill: "
-                         "chunked prefill of 8 x 16384 tokens in chunks of 512, 32q/8kv heads")
+                         "chunked prefill of 8 x 16384 tokens in chunks of 512, 32q/8kv heads; "
+                         "replicate: one 2048-token, 32-layer prompt cache copied into 64 rows; "
+                         "mixed: the KV path of one decode step of a 24-layer mixed-window, "
+                         "KV-sharing stack at B=16, context 4096")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain device copy of COPY_BYTES, ten times (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -196,6 +200,165 @@ def cpu_prefill_baseline(q, k, v, budget_s=15.0):
                       f"{len(times)} runs; torch CPU SDPA restatement of the reference fallback"}
 
 
+RP_SLOTS, RP_P, RP_ROWS, RP_T, RP_HKV = 32, 2048, 64, 2560, 8
+
+
+def bench_replicate(args):
+    """KVCache.prefill: a batch-1 cache holding a 2048-token prompt in 32 slots (8 KV heads,
+    head_dim 128, bf16) replicated into the first 2048 positions of a 64-row cache of 2560
+    positions. One step = one prefill() call."""
+    import torch
+    from modelcore_amd import stats
+    from modelcore_amd.cache import KVCache
+
+    W, K = min(args.warmup, 3), max(1, min(args.steps, 20))
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    log(f"replication: {RP_SLOTS} slots x {RP_P} tokens x {RP_HKV} heads -> {RP_ROWS} rows")
+    src = KVCache(1, RP_HKV, RP_P, D, RP_SLOTS, dev, torch.bfloat16)
+    src.k_cache.copy_(torch.randn(src.k_cache.shape, generator=g, device=dev))
+    src.v_cache.copy_(torch.randn(src.v_cache.shape, generator=g, device=dev))
+    src.advance(RP_P)
+    dst = KVCache(RP_ROWS, RP_HKV, RP_T, D, RP_SLOTS, dev, torch.bfloat16)
+
+    def step():
+        dst.reset()
+        dst.prefill(src)
+
+    for _ in range(W):
+        step()
+    torch.cuda.synchronize()
+    assert torch.equal(dst.k_cache[:, RP_ROWS - 1, :RP_P], src.k_cache[:, 0])
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(K):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / K
+    nbytes = stats.replicate_bytes(RP_SLOTS, RP_ROWS, RP_P, RP_HKV, D, 2)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    result = {
+        "metric": "KV replication GB/s: 2048-token prompt cache, 32 layers x 8 kv heads x hd128, "
+                  "into 64 rows; % of HBM peak",
+        "value": round(gbps, 1), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "KVCache.prefill of a batch-1, 2048-token, 32-slot cache into 64 "
+                               "rows of a 2560-position cache",
+                   "slots": RP_SLOTS, "prompt": RP_P, "rows": RP_ROWS, "n_kv_head": RP_HKV,
+                   "head_dim": D},
+        "roofline": {"kernel": "kv_replicate_kernel", "bound": "hbm", "achieved": round(gbps, 1),
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(gbps * 1e9 / HBM_PEAK, 4),
+                     "traffic": None, "bytes_per_launch": nbytes},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_replicate_baseline(src)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_replicate_baseline(src, budget_s=10.0):
+    """The reference's broadcast copy (oracle.sdpa_fallback.replicate: slice assignment of the
+    batch-1 source over all rows) on the host, for 2 of the 32 slots."""
+    import torch
+    from modelcore_amd import stats
+    from oracle import sdpa_fallback
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    n_slots = 2
+    sk, sv = src.k_cache[:n_slots].cpu(), src.v_cache[:n_slots].cpu()
+    dk = torch.zeros(n_slots, RP_ROWS, RP_T, RP_HKV, D, dtype=torch.bfloat16)
+    dv = torch.zeros_like(dk)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+        t0 = time.perf_counter()
+        sdpa_fallback.replicate(dk, dv, sk, sv, RP_P)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    nbytes = stats.replicate_bytes(n_slots, RP_ROWS, RP_P, RP_HKV, D, 2)
+    return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{n_slots} of the {RP_SLOTS} slots, median of {len(times)} runs; torch CPU "
+                      f"slice-assignment broadcast (the reference's KVCache.prefill copy)"}
+
+
+MX_LAYERS, MX_B, MX_H, MX_HKV, MX_P, MX_WIN = 24, 16, 12, 4, 4096, 1024
+
+
+def bench_mixed(args):
+    """The KV path of a 24-layer stack per decode step: layer i has window -1 if i % 4 == 3 else
+    1024; even layers produce K/V into slot i // 2, odd layers read slot (i - 1) // 2 (and
+    rewrite the producer's token there, as the reference's consumer call does). B = 16 rows at
+    position 4096 + step, H = 12, H_kv = 4, head_dim 128, bf16. One step = 24 operator calls plus
+    the cache advance, replayed from a HIP graph."""
+    import torch
+    from modelcore_amd import stats
+    from modelcore_amd.cache import KVCache
+    from modelcore_amd.kernels.flash_attn import flash_attn
+
+    W, K = args.warmup, args.steps
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    n_slots = MX_LAYERS // 2
+    T = MX_P + W + K + 1
+    log(f"mixed-window stack: {MX_LAYERS} layers, {n_slots} slots, B={MX_B}, T={T}")
+    cache = KVCache(MX_B, MX_HKV, T, D, n_slots, dev, torch.bfloat16)
+    cache.k_cache.copy_(torch.randn(cache.k_cache.shape, generator=g, device=dev))
+    cache.v_cache.copy_(torch.randn(cache.v_cache.shape, generator=g, device=dev))
+    cache.advance(MX_P)
+    n = W + K
+    qs = torch.randn(n, MX_LAYERS, MX_B, 1, MX_H, D, generator=g, device=dev).to(torch.bfloat16)
+    ks = torch.randn(n, n_slots, MX_B, 1, MX_HKV, D, generator=g, device=dev).to(torch.bfloat16)
+    vs = torch.randn(n, n_slots, MX_B, 1, MX_HKV, D, generator=g, device=dev).to(torch.bfloat16)
+    windows = [-1 if i % 4 == 3 else MX_WIN for i in range(MX_LAYERS)]
+
+    def step(s):
+        for i in range(MX_LAYERS):
+            slot = i // 2
+            kc, vc = cache.get_slot_cache(slot)
+            flash_attn.flash_attn_with_kvcache(qs[s, i], kc, vc, k=ks[s, slot], v=vs[s, slot],
+                                               cache_seqlens=cache.cache_seqlens, causal=True,
+                                               window_size=(windows[i], 0))
+        cache.advance(1)
+
+    for s in range(W):
+        step(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for s in range(K):
+            step(W + s)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / K
+    total = 0
+    for s in range(K):
+        pos = [MX_P + W + s] * MX_B
+        for w in windows:
+            total += stats.decode_step_bytes(pos, MX_H, MX_HKV, D, 2, window=w)
+    step_bytes = total / K
+    gbps = step_bytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "mixed-window stack decode: KV-path GB/s per step, 24 layers (3:1 local 1024 / "
+                  "global), KV sharing, B=16, ctx 4096, GQA 12/4 hd128",
+        "value": round(MX_B / (ms * 1e-3), 1), "unit": "tok/s", "n_gpus": 1, "steps": K,
+        "warmup": W, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "KV path of one decode step of a 24-layer stack (18 layers window "
+                               "1024, 6 global; odd layers share the previous layer's slot), B=16, "
+                               "positions 4096+", "layers": MX_LAYERS, "batch": MX_B,
+                   "n_head": MX_H, "n_kv_head": MX_HKV, "head_dim": D, "timing": "hip_graph"},
+        "roofline": {"kernel": "decode_fused_kernel + decode_merge_kernel (24 calls per step)",
+                     "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(gbps * 1e9 / HBM_PEAK, 4), "traffic": None,
+                     "bytes_per_step": int(step_bytes)},
+    }), flush=True)
+
+
 def cpu_baseline(kc, vc, q, k, v, seqlens, budget_s=12.0):
     """The reference's CPU fallback (oracle.sdpa_fallback: append + masked SDPA with GQA) on the
     full decode workload, on this host's cores: median seconds per step over a bounded run."""
@@ -227,6 +390,12 @@ def main():
         return
     if args.workload == "prefill":
         bench_prefill(args)
+        return
+    if args.workload == "replicate":
+        bench_replicate(args)
+        return
+    if args.workload == "mixed":
+        bench_mixed(args)
         return
 
     import torch
