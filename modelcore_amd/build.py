@@ -40,6 +40,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source extra flags. The chunked-prefill kernel keeps its score accumulators in VGPRs, where
+# the softmax reads them; without this the allocator parks them in AGPRs and copies them back and
+# forth on every key tile (measured: ~500 v_accvgpr moves per tile).
+SOURCE_FLAGS = {
+    "prefill_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(path):
@@ -53,7 +61,7 @@ def sources() -> list[Path]:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
