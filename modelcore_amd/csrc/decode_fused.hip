@@ -53,7 +53,10 @@ constexpr int kMaxGroups = 1024;      // 4-wave workgroups per launch, at most
 #define MCAMD_DECODE_GROUPS_PER_CU 1
 #endif
 constexpr int kGroupsPerCU = MCAMD_DECODE_GROUPS_PER_CU;  // 1: one wave per SIMD
-constexpr int kMinKeysPerGroup = 256; // fewer workgroups when the whole job is small
+#ifndef MCAMD_DECODE_MIN_KEYS
+#define MCAMD_DECODE_MIN_KEYS 64
+#endif
+constexpr int kMinKeysPerGroup = MCAMD_DECODE_MIN_KEYS;  // fewer workgroups when the job is small
 #ifndef MCAMD_DECODE_RING
 #define MCAMD_DECODE_RING 2
 #endif
