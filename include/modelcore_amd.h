@@ -124,6 +124,21 @@ int mcamd_prefill_attention(const void *q, const void *k_cache, const void *v_ca
                             int64_t t_max, int64_t cache_batch_stride, int64_t window,
                             int dtype, void *stream);
 
+/*
+ * Next-token sampling on the device, one token per row of `logits` ((batch, vocab) fp32, rows
+ * `row_stride` elements apart): temperature 0 takes the argmax (lowest index on ties); otherwise
+ * the Gumbel-max draw from softmax(logits / temperature) with Philox4x32-10 noise keyed by the
+ * row's 64-bit `seeds[b]` at counter offsets[b], which the call then advances by one (device
+ * side, no host sync). Writes int64 token ids to out[b].
+ * Replaces sample_next_token's softmax + torch.multinomial (modelcore/generate.py:18-34); the
+ * per-row counter stream stands in for its single torch.Generator, so a row's draws do not depend
+ * on the batch it is decoded in. top_k is not supported here (the reference's top_k path stays a
+ * torch op in modelcore_amd.generate.sample_next_token).
+ */
+int mcamd_sample_tokens(const float *logits, int64_t batch, int64_t vocab, int64_t row_stride,
+                        float temperature, const uint64_t *seeds, int64_t *offsets, int64_t *out,
+                        void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -44,6 +44,8 @@ SIGNATURES = {
                                       _i64, _i64, _int, _ptr, _size, _ptr]),
     "mcamd_prefill_attention": (_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64,
                                        _i64, _i64, _i64, _i64, _int, _ptr]),
+    "mcamd_sample_tokens": (_int, [_ptr, _i64, _i64, _i64, ctypes.c_float, _ptr, _ptr, _ptr,
+                                   _ptr]),
 }
 
 _LIB = None
