@@ -42,13 +42,15 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
-    ap.add_argument("--workload", choices=("decode", "prefill", "replicate", "mixed"),
+    ap.add_argument("--workload", choices=("decode", "prefill", "replicate", "mixed", "sample"),
                     default="decode",
                     help="decode: the decode microbench (default, the headline metric); prefill: "
                          "chunked prefill of 8 x 16384 tokens in chunks of 512, 32q/8kv heads; "
                          "replicate: one 2048-token, 32-layer prompt cache copied into 64 rows; "
                          "mixed: the KV path of one decode step of a 24-layer mixed-window, "
-                         "KV-sharing stack at B=16, context 4096")
+                         "KV-sharing stack at B=16, context 4096; sample: a 32-layer 4096-wide "
+                         "model prefills one 2048-token prompt, replicates it to 64 rows and "
+                         "samples 512 tokens per row at temperature 1")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain device copy of COPY_BYTES, ten times (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -359,6 +361,90 @@ def bench_mixed(args):
     }), flush=True)
 
 
+SM_LAYERS, SM_D, SM_H, SM_HKV, SM_HID, SM_V = 32, 4096, 32, 8, 14336, 32768
+SM_PROMPT, SM_ROWS, SM_NEW = 2048, 64, 512
+
+
+def bench_sample(args):
+    """Large-batch sampling end to end: a 32-layer model (d_model 4096, 32 q / 8 kv heads of 128,
+    gated SiLU MLP 14336, vocab 32768, softcap 15, bf16, random init with seed 0) prefills one
+    2048-token prompt (uniform random tokens, seed 0) at batch 1, replicates its cache into 64
+    rows (KVCache.prefill), then decodes 512 tokens per row, each drawn on the device at
+    temperature 1.0 from a per-row Philox stream (row r seeded r). The first --warmup steps are
+    untimed; the value is rows x timed steps / time."""
+    import torch
+    from modelcore_amd import stats
+    from modelcore_amd.model import ComponentSpec, ModelConfig, ModelManager
+    from modelcore_amd.runtime import Runtime
+    from modelcore_amd.sampling import PhiloxSampler
+
+    dev = torch.device("cuda", 0)
+    W = min(args.warmup, SM_NEW - 1)
+    K = SM_NEW - W
+    blocks = [ComponentSpec("block", {
+        "layer_idx": i, "features": [],
+        "mixer": ComponentSpec("attention", {"n_head": SM_H, "n_kv_head": SM_HKV, "head_dim": D,
+                                             "window": -1, "kv_slot": None, "produces_kv": True,
+                                             "features": []}),
+        "ffn": ComponentSpec("gated_mlp", {"activation": "silu", "hidden_dim": SM_HID})})
+        for i in range(SM_LAYERS)]
+    cfg = ModelConfig(sequence_len=SM_PROMPT + SM_NEW, vocab_size=SM_V, n_embd=SM_D,
+                      shared={"rope": ComponentSpec("rotary", {"head_dim": D, "over_compute": 2}),
+                              "norm": ComponentSpec("rms_norm", {"eps": None})},
+                      input=ComponentSpec("token_embedding", {"smear": False}),
+                      body=ComponentSpec("stack", {"blocks": blocks, "features": []}),
+                      output=ComponentSpec("lm_head", {"softcap": 15}))
+    mgr = ModelManager(Runtime(torch.bfloat16))
+    log(f"building the {SM_LAYERS}-layer model on the GPU (seed 0)")
+    model = mgr.create_model(cfg, device=dev, seed=0)
+    model.cache_inference_weights()
+    prompt = torch.randint(0, SM_V, (SM_PROMPT,), generator=torch.Generator().manual_seed(0))
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    dec = mgr.new_decoder(model, prompt.tolist(), num_samples=SM_ROWS, max_tokens=SM_NEW)
+    end.record()
+    torch.cuda.synchronize()
+    prefill_ms = start.elapsed_time(end)
+    sampler = PhiloxSampler(SM_ROWS, dev, base_seed=0)
+    log(f"prefill + replicate {prefill_ms:.1f} ms; decoding {W} + {K} steps")
+    with torch.inference_mode():
+        for _ in range(W):
+            dec.step(sampler(dec.logits, 1.0).view(-1))
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(K):
+            dec.step(sampler(dec.logits, 1.0).view(-1))
+        end.record()
+        torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / K
+    assert dec.kv_cache.get_pos() == SM_PROMPT + SM_NEW
+    weight_bytes = sum(m._cast.numel() * m._cast.element_size() for m in model.modules()
+                       if getattr(m, "_cast", None) is not None)
+    kv = sum(stats.decode_step_bytes([SM_PROMPT + W + i] * SM_ROWS, SM_H, SM_HKV, D, 2)
+             for i in range(K)) / K * SM_LAYERS
+    step_bytes = weight_bytes + kv
+    gbps = step_bytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "large-batch sampling tok/s: 32-layer 4096-wide model, one 2048-token prompt "
+                  "replicated to 64 rows, 512 tokens per row at temperature 1",
+        "value": round(SM_ROWS / (ms * 1e-3), 1), "unit": "tok/s", "n_gpus": 1, "steps": K,
+        "warmup": W, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "batch-1 prefill of 2048 tokens, KVCache.prefill to 64 rows, "
+                               "then one model forward + device sampling per step",
+                   "layers": SM_LAYERS, "d_model": SM_D, "n_head": SM_H, "n_kv_head": SM_HKV,
+                   "head_dim": D, "mlp_hidden": SM_HID, "vocab": SM_V, "rows": SM_ROWS,
+                   "prompt": SM_PROMPT, "new_tokens": SM_NEW,
+                   "prefill_and_replicate_ms": round(prefill_ms, 2)},
+        "roofline": {"kernel": "whole decode step (bf16 weight GEMMs + cached attention of 32 "
+                               "layers + sampling)", "bound": "hbm", "achieved": round(gbps, 1),
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(gbps * 1e9 / HBM_PEAK, 4), "traffic": None,
+                     "bytes_per_step": int(step_bytes), "weight_bytes": int(weight_bytes)},
+    }), flush=True)
+
+
 def cpu_baseline(kc, vc, q, k, v, seqlens, budget_s=12.0):
     """The reference's CPU fallback (oracle.sdpa_fallback: append + masked SDPA with GQA) on the
     full decode workload, on this host's cores: median seconds per step over a bounded run."""
@@ -396,6 +482,9 @@ def main():
         return
     if args.workload == "mixed":
         bench_mixed(args)
+        return
+    if args.workload == "sample":
+        bench_sample(args)
         return
 
     import torch

@@ -126,7 +126,7 @@ int mcamd_prefill_attention(const void *q, const void *k_cache, const void *v_ca
 
 /*
  * Next-token sampling on the device, one token per row of `logits` ((batch, vocab) fp32, rows
- * `row_stride` elements apart): temperature 0 takes the argmax (lowest index on ties); otherwise
+ * `row_stride` elements apart; 0 = every row reads the same logits): temperature 0 takes the argmax (lowest index on ties); otherwise
  * the Gumbel-max draw from softmax(logits / temperature) with Philox4x32-10 noise keyed by the
  * row's 64-bit `seeds[b]` at counter offsets[b], which the call then advances by one (device
  * side, no host sync). Writes int64 token ids to out[b].

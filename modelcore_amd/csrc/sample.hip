@@ -125,8 +125,9 @@ using namespace mcamd;
 extern "C" int mcamd_sample_tokens(const float *logits, int64_t batch, int64_t vocab,
                                    int64_t row_stride, float temperature, const uint64_t *seeds,
                                    int64_t *offsets, int64_t *out, void *stream) {
-  if (batch < 0 || vocab <= 0 || vocab > (int64_t(1) << 30) || row_stride < vocab)
-    return fail(MCAMD_EINVAL, "sample_tokens: need batch >= 0, 0 < vocab <= 2^30, row_stride >= vocab");
+  if (batch < 0 || vocab <= 0 || vocab > (int64_t(1) << 30) || (row_stride != 0 && row_stride < vocab))
+    return fail(MCAMD_EINVAL,
+                "sample_tokens: need batch >= 0, 0 < vocab <= 2^30, row_stride 0 or >= vocab");
   if (!(temperature >= 0.f) || std::isinf(temperature))
     return fail(MCAMD_EINVAL, "sample_tokens: temperature must be finite and non-negative");
   if (batch > 0 && (!logits || !seeds || !offsets || !out))

@@ -103,10 +103,16 @@ class AttentionLayerSpec:
 # Components
 # -----------------------------------------------------------------------------------------------
 class Linear(nn.Linear):
-    """fp32 master weight, cast to the activation dtype at every call."""
+    """fp32 master weight, cast to the activation dtype at every call -- or, after
+    ``Model.cache_inference_weights``, read from a copy cast once (the same values, without the
+    per-call cast traffic)."""
+    _cast = None
 
     def forward(self, x):
-        return F.linear(x, self.weight.to(dtype=x.dtype))
+        w = self._cast
+        if w is None or w.dtype != x.dtype:
+            w = self.weight.to(dtype=x.dtype)
+        return F.linear(x, w)
 
 
 class RMSNorm(nn.Module):
@@ -489,6 +495,23 @@ class Model(nn.Module):
             m.init_weights()
         self.body.init_weights()
         self.unembedding.init_weights()
+
+    @torch.no_grad()
+    def cache_inference_weights(self, dtype=None):
+        """Keep a copy of every Linear weight in `dtype` (default: the compute dtype) and use it
+        instead of casting the fp32 master weight at every call. The products are bit-identical
+        (the cast is the same); the per-step weight traffic of a decode drops from a read of the
+        fp32 weights plus a write and a read of the cast copy to one read of the copy. Call again
+        after the master weights change; ``drop_inference_weights`` undoes it."""
+        dtype = dtype or self.runtime.compute_dtype
+        for m in self.modules():
+            if isinstance(m, Linear):
+                m._cast = m.weight.detach().to(dtype)
+
+    def drop_inference_weights(self):
+        for m in self.modules():
+            if isinstance(m, Linear):
+                m._cast = None
 
     def layer_specs(self):
         return [b.mixer.layer_spec() for b in self.body.blocks]

@@ -42,8 +42,8 @@ class PhiloxSampler:
             raise ValueError("temperature must be non-negative")
         if logits.dtype != torch.float32:
             logits = logits.float()
-        if logits.stride(1) != 1:
-            logits = logits.contiguous()
+        if logits.stride(1) != 1 or 0 < logits.stride(0) < logits.size(1):
+            logits = logits.contiguous()  # a stride-0 (expanded) batch is read as is
         out = torch.empty(self.batch_size, dtype=torch.int64, device=logits.device)
         st = _ext.lib().mcamd_sample_tokens(
             logits.data_ptr(), self.batch_size, logits.size(1), logits.stride(0),

@@ -161,3 +161,48 @@ def test_mixed_window_kv_sharing_stack_in_bf16(cpu_cache_copies):
         print(f"call {i}: logits max-abs {err:.4f} (scale {b.abs().max().item():.3f})", flush=True)
         assert err <= 0.15, f"call {i}: logits max-abs {err}"
     assert gpu_cache.cache_seqlens.tolist() == [P + steps] * B
+
+
+def test_sampling_decoder_rows_are_replicas_and_draws_are_reproducible():
+    """The large-batch sampling flow at small scale (bf16, GQA 12/4, head_dim 128): one prompt
+    prefilled at batch 1 and replicated to 8 rows gives 8 bit-identical caches and identical
+    first logits; device sampling with per-row seeds then decodes the same tokens on a rerun, and
+    rows that happen to draw the same tokens keep identical logits."""
+    from modelcore_amd.sampling import PhiloxSampler
+    _note("sampling decoder")
+    cfg = mixed_window_config(n_layer=4)
+    mgr = gpu_manager(torch.bfloat16)
+    model = mgr.create_model(cfg, device=DEV, seed=0)
+    awake(model)
+    model.cache_inference_weights()
+    prompt = torch.randint(0, cfg.vocab_size, (150,), generator=torch.Generator().manual_seed(2))
+
+    def run():
+        dec = mgr.new_decoder(model, prompt.tolist(), num_samples=8, max_tokens=12)
+        kc = dec.kv_cache.k_cache
+        assert all(torch.equal(kc[:, r, :150], kc[:, 0, :150]) for r in range(8))
+        assert torch.equal(dec.logits, dec.logits[:1].expand(8, -1))
+        sampler = PhiloxSampler(8, DEV, base_seed=40)
+        toks = []
+        for _ in range(12):
+            t = sampler(dec.logits, 1.0).view(-1)
+            toks.append(t.cpu())
+            dec.step(t)
+        return torch.stack(toks, dim=1)
+
+    a, b = run(), run()
+    assert torch.equal(a, b)
+    assert len({tuple(r.tolist()) for r in a}) > 1  # different seeds diverge
+
+
+def test_cached_inference_weights_give_identical_logits():
+    cfg = mixed_window_config(n_layer=2)
+    mgr = gpu_manager(torch.bfloat16)
+    model = awake(mgr.create_model(cfg, device=DEV, seed=0))
+    idx = torch.randint(0, cfg.vocab_size, (2, 40), generator=torch.Generator().manual_seed(3)).to(DEV)
+    with torch.no_grad():
+        a = model(idx)
+        model.cache_inference_weights()
+        b = model(idx)
+        model.drop_inference_weights()
+    assert torch.equal(a, b)
