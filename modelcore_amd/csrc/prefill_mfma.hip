@@ -29,8 +29,11 @@
 // maximum exceeds it by more than 2^8, so most tiles skip the rescale of O. Tiles entirely inside
 // every pair's visible range skip the masking.
 //
-// LDS: three buffers of one K and one V tile (64 keys x 256 bytes each), filled straight from
-// HBM by global_load_lds_dwordx4 (no registers involved) one tile ahead of its first use.
+// LDS: four buffers of one K and one V tile (64 keys x 256 bytes each), filled straight from
+// HBM by buffer_load_dwordx4 ... lds (no registers involved) two tiles ahead of their first use;
+// the buffer resource bounds every read to the (row, KV head)'s cache and keeps the per-lane
+// address arithmetic in 32 bits. Each wave issues its four loads of a tile spread over its work
+// of the slot, so no wave stalls on a full memory queue.
 //  * K is stored fragment-major: 16 blocks of 1 KiB, block (mk, kd) holding exactly the A
 //    fragment of keys 32 mk .. + 31 and dims 16 kd .. + 15 in lane order, so a wave reads a
 //    fragment as one contiguous 1 KiB.
@@ -38,9 +41,12 @@
 //    which the transpose reads (4 consecutive rows, 32 bytes each per 16 lanes) use every bank.
 // Both layouts were chosen by measuring the access patterns on MI355X (64 B/clk for row-strided
 // 16-byte reads against ~100 B/clk contiguous; 134 B/clk for the swizzled transpose reads).
+// In the matrix phase the LDS reads of the next 16-key step are issued (as inline asm, with
+// explicit waits) before the products of the current one, so the LDS streams under the MFMAs.
 #include "kernels.h"
 
 #include <cmath>
+#include <type_traits>
 
 namespace mcamd {
 namespace {
@@ -83,11 +89,32 @@ __device__ __forceinline__ bf16x4 lds_read_tr(const uint16_t *p) {
 // Swizzle of the 16-byte chunks of V row r (0..63): chunk c is stored at slot c ^ swz(r).
 __device__ __forceinline__ int swz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
 
-// One direct HBM -> LDS load: lane i's 16 bytes land at lds_wave_base + 16 i.
-__device__ __forceinline__ void dma16(const uint16_t *src, uint16_t *lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1))) *)(src),
-                                   (void __attribute__((address_space(3))) *)(lds_wave_base), 16,
-                                   0, 0);
+// LDS byte address of a pointer into shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return uint32_t(uintptr_t((const __attribute__((address_space(3))) void *)(p)));
+}
+// LDS reads issued as inline asm so they keep their place in the instruction stream. The
+// compiler does not track them: every use of their results sits behind an explicit
+// `s_waitcnt lgkmcnt(0)` asm that takes those results as operands (wait_all in the kernel).
+template <int OFF>
+__device__ __forceinline__ void ds_read_b128(bf16x8 &d, uint32_t addr) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "i"(OFF));
+}
+template <int OFF>
+__device__ __forceinline__ void ds_read_tr(bf16x4 &d, uint32_t addr) {
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "i"(OFF));
+}
+
+// Across the two 32-lane halves of the wave (lane l with lane l ^ 32), on the VALU.
+__device__ __forceinline__ float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ __forceinline__ float exp2_or_zero(float x) {
@@ -95,8 +122,8 @@ __device__ __forceinline__ float exp2_or_zero(float x) {
 }
 
 __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P) {
-  __shared__ __attribute__((aligned(1024))) uint16_t sK[3][TILE];
-  __shared__ __attribute__((aligned(1024))) uint16_t sV[3][TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t sK[4][TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t sV[4][TILE];
 
   const int bh = blockIdx.x % P.n_bh;
   const int qt = blockIdx.x / P.n_bh;
@@ -146,16 +173,38 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
   // A tile takes 32 DMA instructions of 1 KiB (16 K fragments, 16 blocks of 4 V rows); wave w
   // issues K fragments 2w, 2w + 1 and V blocks 2w, 2w + 1. Keys past `hi` re-read key `hi` (they
   // are masked).
+  // K/V of this (row, KV head) as buffer resources: 32-bit byte offsets from the head's first
+  // element, bounded by the last key of the cache (out-of-range reads would return zero).
+  const uint32_t tok_bytes = uint32_t(tok) * 2u;
+  const uint32_t extent = uint32_t(P.T_max - 1) * tok_bytes + uint32_t(D) * 2u;
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc((void *)kbase, 0, int(extent), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc((void *)vbase, 0, int(extent), 0x00020000);
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t k_lane_off = uint32_t(8 * h) * 2u;
+  const uint32_t v_chunk = uint32_t((lane & 15) ^ (4 * ((lane >> 4) & 3)));
+  // Part i (0..3) of this wave's share of a tile: K fragment 2w + i / 2 (i even) or V block
+  // 2w + i / 2 (i odd).
+  auto issue_part = [&](int k0, int buf, int i) {
+    const int f = 2 * wave_s + (i >> 1);
+    if ((i & 1) == 0) {
+      const uint32_t kkey = uint32_t(min(k0 + 32 * (f >> 3) + col, hi));
+      const uint32_t off = __umul24(kkey, tok_bytes) + uint32_t(16 * (f & 7)) * 2u + k_lane_off;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rk, (__attribute__((address_space(3))) void *)(&sK[buf][f * 512]), 16, int(off), 0, 0,
+          0);
+    } else {
+      const uint32_t vkey = uint32_t(min(k0 + 4 * f + (lane >> 4), hi));  // row 4f + lane / 16
+      const uint32_t off = __umul24(vkey, tok_bytes) + ((v_chunk ^ uint32_t(f & 3)) << 4);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rv, (__attribute__((address_space(3))) void *)(&sV[buf][f * 512]), 16, int(off), 0, 0,
+          0);
+    }
+  };
   auto issue_tile = [&](int k0, int buf) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int f = 2 * wave + j;  // K fragment (mk, kd) = (f / 8, f % 8)
-      const int kkey = min(k0 + 32 * (f >> 3) + col, hi);
-      dma16(kbase + int64_t(kkey) * tok + 16 * (f & 7) + 8 * h, &sK[buf][f * 512]);
-      const int r = 4 * f + (lane >> 4);  // V block f = rows 4f .. 4f + 3
-      const int vkey = min(k0 + r, hi);
-      dma16(vbase + int64_t(vkey) * tok + (((lane & 15) ^ swz(r)) << 3), &sV[buf][f * 512]);
-    }
+    for (int i = 0; i < 4; ++i) issue_part(k0, buf, i);
   };
 
   f32x16 o[4];
@@ -169,6 +218,17 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
   const int L16 = lane & 15;
   const int tr_row = L16 >> 2;
   const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (L16 & 3);
+  // Byte offsets of this lane's transpose reads in a V tile for 16-key step 0 (rows r0 = 4h +
+  // tr_row and r0 + 8); step ks adds 4096 ks bytes, since the swizzle of rows 16 ks + r does not
+  // depend on ks.
+  uint32_t vofs[8];
+#pragma unroll
+  for (int md = 0; md < 4; ++md) {
+    const int r0 = 4 * h + tr_row, r1 = r0 + 8;
+    const int cc = 32 * md + tr_col;
+    vofs[md] = 2 * (r0 * D + (((cc >> 3) ^ swz(r0)) << 3) + (cc & 7));
+    vofs[4 + md] = 2 * (r1 * D + (((cc >> 3) ^ swz(r1)) << 3) + (cc & 7));
+  }
 
   // Scores of one tile: s[mk][4j + i] is key k0 + 32 mk + 8 j + 4 h + i of pair `col`.
   auto scores = [&](f32x16 (&s)[2], const uint16_t *tK) {
@@ -200,12 +260,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
           if (!ok) s[mk][e] = -INFINITY;
         }
     }
-    float mx = -INFINITY;
+    // Four independent chains, then across the two lane halves on the VALU.
+    float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
     for (int mk = 0; mk < 2; ++mk)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[mk][e]);
-    return fmaxf(mx, __shfl_xor(mx, 32, 64)) * P.scale_log2;
+      for (int e = 0; e < 16; ++e) m4[e & 3] = fmaxf(m4[e & 3], s[mk][e]);
+    return max_halves(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]))) * P.scale_log2;
   };
   // O^T += V^T . P^T for 16-key step ks, in the accumulators' key order.
   auto pv_step = [&](const bf16x8 &pk, int ks, const uint16_t *tV) {
@@ -223,35 +284,54 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
   // Weights of 16-key step ks as the P^T fragment (and their sum into l).
   auto weights = [&](const f32x16 (&s)[2], int ks, float m_use) {
     f32x8 pv;
+    float l2[2] = {0.f, 0.f};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float pe = __builtin_amdgcn_exp2f(fmaf(s[ks >> 1][8 * (ks & 1) + e], P.scale_log2, -m_use));
+      const float pe =
+          __builtin_amdgcn_exp2f(fmaf(s[ks >> 1][8 * (ks & 1) + e], P.scale_log2, -m_use));
       pv[e] = pe;
-      l += pe;
+      l2[e & 1] += pe;
     }
+    l += l2[0] + l2[1];
     return __builtin_convertvector(pv, bf16x8);
   };
 
-  // Ping-pong schedule over tiles of 64 keys, three LDS buffers. Each wave alternates a matrix
+  // Ping-pong schedule over tiles of 64 keys, four LDS buffers. Each wave alternates a matrix
   // phase M(t) -- the scores of tile t + 1 and the P . V of tile t -- with a vector phase V(t) --
   // masks, maximum, rescale and weights of tile t. Waves 0-3 run one phase ahead of waves 4-7
   // (their SIMD partners), so in every slot between two barriers one wave of each SIMD feeds
   // the matrix core while the other works the VALU. Slot 0 holds the first scores of group A,
   // group B starts one slot later and ends one slot later; both cross 2 n + 2 barriers.
-  // Tile j is fetched at slot 2 j - 2 into buffer j % 3 and is read in slots 2 j .. 2 j + 3.
+  // Tile j (j >= 2) is fetched during slot 2 j - 4 into buffer j % 4 and is read in slots
+  // 2 j .. 2 j + 3; tiles 0 and 1 are fetched before the loop.
   const int n_tiles = (hi - lo) / KT + 1;
   const int lag = wave >= 4 ? 1 : 0;
   issue_tile(lo, 0);
+  if (n_tiles > 1) issue_tile(lo + KT, 1);
   f32x16 sc[2];
   bf16x8 pk[4];
   for (int slot = 0; slot < 2 * n_tiles + 2; ++slot) {
-    if ((slot & 1) == 0) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): tile slot / 2 landed
+    if ((slot & 1) == 0) {
+      // Tile slot / 2 has landed once only the four DMAs of tile slot / 2 + 1 may be pending.
+      if (slot / 2 + 1 < n_tiles)
+        __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
+      else
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    }
     __syncthreads();
-    if ((slot & 1) == 0 && slot / 2 + 1 < n_tiles)
-      issue_tile(lo + (slot / 2 + 1) * KT, (slot / 2 + 1) % 3);
+    // Even slots fetch tile slot / 2 + 2 into buffer (slot / 2 + 2) % 4, whose previous tile was
+    // last read in slot - 1; the four parts are spread over the slot's work.
+    const int dma_tile = ((slot & 1) == 0 && slot / 2 + 2 < n_tiles) ? slot / 2 + 2 : -1;
+    auto dma_part = [&](int i) {
+      if (dma_tile >= 0) issue_part(lo + dma_tile * KT, dma_tile % 4, i);
+    };
     const int ph = slot - lag;  // this wave's phase index
-    if (ph < 0 || ph > 2 * n_tiles) continue;
+    if (ph < 0 || ph > 2 * n_tiles) {
+      for (int i = 0; i < 4; ++i) dma_part(i);
+      continue;
+    }
     if (ph == 0) {
+      for (int i = 0; i < 4; ++i) dma_part(i);
       scores(sc, sK[0]);
     } else if (ph & 1) {
       const int t = (ph - 1) / 2;  // V(t)
@@ -268,38 +348,75 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
       }
       const float m_use = m == -INFINITY ? 0.f : m;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) pk[ks] = weights(sc, ks, m_use);
+      for (int ks = 0; ks < 4; ++ks) {
+        pk[ks] = weights(sc, ks, m_use);
+        dma_part(ks);
+      }
     } else {
       const int t = ph / 2 - 1;  // M(t)
       if (t + 1 < n_tiles) {
-        // The two products interleaved, 16 key-steps / dims at a time, so the matrix core has
-        // six independent accumulation chains in flight (two score blocks, four output blocks).
-        const uint16_t *tK = sK[(t + 1) % 3];
+        // The two products interleaved; the twelve LDS reads of step ks + 1 (four K fragments,
+        // four V^T fragments of two transpose reads) are issued before the eight products of
+        // step ks, so the reads stream while the matrix core works.
+        const uint32_t ka = lds_addr(&sK[(t + 1) % 4][lane * 8]);
+        const uint32_t vb = lds_addr(sV[t % 4]);
+        uint32_t va[8];
 #pragma unroll
-        for (int mk = 0; mk < 2; ++mk)
+        for (int i = 0; i < 8; ++i) va[i] = vb + vofs[i];
+        bf16x8 kf[2][4];
+        bf16x4 vf[2][4][2];
+        auto issue = [&](auto ks_c, int buf) {
+          constexpr int ks = decltype(ks_c)::value;
+          ds_read_b128<(0 * 8 + 2 * ks) * 1024>(kf[buf][0], ka);
+          ds_read_b128<(1 * 8 + 2 * ks) * 1024>(kf[buf][1], ka);
+          ds_read_b128<(0 * 8 + 2 * ks + 1) * 1024>(kf[buf][2], ka);
+          ds_read_b128<(1 * 8 + 2 * ks + 1) * 1024>(kf[buf][3], ka);
 #pragma unroll
-          for (int e = 0; e < 16; ++e) sc[mk][e] = 0.f;
+          for (int md = 0; md < 4; ++md) {
+            ds_read_tr<4096 * ks>(vf[buf][md][0], va[md]);
+            ds_read_tr<4096 * ks>(vf[buf][md][1], va[4 + md]);
+          }
+        };
+        auto wait_all = [&](int buf) {
+          asm volatile("s_waitcnt lgkmcnt(0)"
+                       : "+v"(kf[buf][0]), "+v"(kf[buf][1]), "+v"(kf[buf][2]), "+v"(kf[buf][3]),
+                         "+v"(vf[buf][0][0]), "+v"(vf[buf][0][1]), "+v"(vf[buf][1][0]),
+                         "+v"(vf[buf][1][1]), "+v"(vf[buf][2][0]), "+v"(vf[buf][2][1]),
+                         "+v"(vf[buf][3][0]), "+v"(vf[buf][3][1]));
+        };
+        const f32x16 zero16 = {};
+        auto step = [&](auto ks_c) {
+          constexpr int ks = decltype(ks_c)::value;
+          constexpr int cur = ks & 1;
+          wait_all(cur);
+          if constexpr (ks < 3) issue(std::integral_constant<int, ks + 1>{}, cur ^ 1);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-          for (int kd = 2 * ks; kd < 2 * ks + 2; ++kd)
-#pragma unroll
-            for (int mk = 0; mk < 2; ++mk) {
-              const bf16x8 a = __builtin_bit_cast(
-                  bf16x8, *reinterpret_cast<const uint4 *>(&tK[(mk * 8 + kd) * 512 + lane * 8]));
-              sc[mk] = mfma(a, qf[kd], sc[mk]);
-            }
-          pv_step(pk[ks], ks, sV[t % 3]);
-        }
+          for (int i = 0; i < 4; ++i) {
+            const int mk = i & 1, kd = 2 * ks + (i >> 1);
+            sc[mk] = mfma(kf[cur][i], qf[kd], kd == 0 ? zero16 : sc[mk]);
+            const bf16x8 a = __builtin_shufflevector(vf[cur][i][0], vf[cur][i][1], 0, 1, 2, 3, 4,
+                                                     5, 6, 7);
+            o[i] = mfma(a, pk[ks], o[i]);
+          }
+          dma_part(ks);
+        };
+        issue(std::integral_constant<int, 0>{}, 0);
+        step(std::integral_constant<int, 0>{});
+        step(std::integral_constant<int, 1>{});
+        step(std::integral_constant<int, 2>{});
+        step(std::integral_constant<int, 3>{});
       } else {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) pv_step(pk[ks], ks, sV[t % 3]);
+        for (int ks = 0; ks < 4; ++ks) {
+          pv_step(pk[ks], ks, sV[t % 4]);
+          dma_part(ks);
+        }
       }
     }
   }
 
   // Normalise and write: o[md][4j + i] is dim 32 md + 8 j + 4 h + i of pair `col`.
-  const float lt = l + __shfl_xor(l, 32, 64);
+  const float lt = sum_halves(l);
   const float inv = 1.f / lt;
   if (!live) return;
 #pragma unroll
@@ -321,7 +438,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
 }  // namespace
 
 bool prefill_mfma_supported(const AttnArgs &a) {
-  return a.dtype == MCAMD_BF16 && a.head_dim == D && a.n_head / a.n_kv_head <= kPairs;
+  // Byte offsets within one (row, KV head) must fit the 32-bit buffer offsets.
+  const int64_t extent = ((a.t_max - 1) * a.n_kv_head * D + D) * 2;
+  return a.dtype == MCAMD_BF16 && a.head_dim == D && a.n_head / a.n_kv_head <= kPairs &&
+         a.n_kv_head < 65536 && extent < (int64_t(1) << 31);
 }
 
 int launch_prefill_mfma(const AttnArgs &a) {
@@ -349,3 +469,4 @@ int launch_prefill_mfma(const AttnArgs &a) {
 }
 
 }  // namespace mcamd
+
