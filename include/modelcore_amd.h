@@ -139,6 +139,27 @@ int mcamd_sample_tokens(const float *logits, int64_t batch, int64_t vocab, int64
                         float temperature, const uint64_t *seeds, int64_t *offsets, int64_t *out,
                         void *stream);
 
+/*
+ * The step before the operator, fused: RoPE at each token's position p = cache_seqlens[b] + t,
+ * RMS-norm over head_dim (eps added to the mean square, fp32 arithmetic), and `scale`, applied to
+ * q (written to q_out, (batch, t_new, n_head, head_dim)) and to k, which is then appended with v
+ * at p as mcamd_kv_append does. `cos`/`sin` are the rotary tables, (n_pos, head_dim / 2) in the
+ * storage dtype. k = v = NULL transforms q only (k_cache/v_cache unused). Each rotation product
+ * and sum is rounded to the storage dtype like the separate torch ops; only the order of the
+ * fp32 sum of squares differs from them (results within one unit in the last place).
+ * Replaces, in modelcore/components/attention.py:143-150 (producer layers) and :155-157
+ * (KV-sharing consumers): RotaryEmbedding.forward/apply_to_q (modelcore/components/rotary.py:
+ * 69-81 -> rope.py:4-12), the QK RMSNorm (modelcore/components/norm.py:43-44), the two x1.2
+ * multiplies, and the append half of flash_attn_with_kvcache (modelcore/kernels/flash_attn.py:
+ * 336-346). Positions come from cache_seqlens on the device: no host sync.
+ */
+int mcamd_qk_rope_norm_append(const void *q, const void *k, const void *v, const void *cos,
+                              const void *sin, int64_t n_pos, void *k_cache, void *v_cache,
+                              const int32_t *cache_seqlens, void *q_out, int64_t batch,
+                              int64_t t_new, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
+                              int64_t t_max, int64_t cache_batch_stride, float eps, float scale,
+                              int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

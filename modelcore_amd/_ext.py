@@ -46,6 +46,9 @@ SIGNATURES = {
                                        _i64, _i64, _i64, _i64, _int, _ptr]),
     "mcamd_sample_tokens": (_int, [_ptr, _i64, _i64, _i64, ctypes.c_float, _ptr, _ptr, _ptr,
                                    _ptr]),
+    "mcamd_qk_rope_norm_append": (_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _ptr,
+                                         _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                         ctypes.c_float, ctypes.c_float, _int, _ptr]),
 }
 
 _LIB = None

@@ -1,0 +1,112 @@
+"""The step before the cached-attention operator, fused into one HIP launch: RoPE at each token's
+cache position, QK RMS-norm, the x1.2 scale, and the append of the new K/V.
+
+It replaces, in an attention layer's forward (modelcore/components/attention.py:143-150 for
+producer layers, :155-157 for KV-sharing consumers), the calls
+
+    q, k = rope(q, k, kv_cache)          # modelcore/components/rotary.py:69-81, rope.py:4-12
+    q, k = norm(q), norm(k)              # modelcore/components/norm.py:43-44 (F.rms_norm)
+    q, k = q * 1.2, k * 1.2
+    ... flash_attn_with_kvcache(..., k=k, v=v, ...)   # its append half, flash_attn.py:336-346
+
+with ``q = rope_norm_scale_append(q, cos, sin, cache_seqlens, k, v, k_cache, v_cache)`` followed
+by the operator with ``k = v = None``. Positions are read from ``cache_seqlens`` on the device
+(p = cache_seqlens[b] + t), so the call never syncs the host and can sit in a captured graph.
+
+Numerics: every rotation product and sum is rounded to the storage dtype as the separate torch
+ops round them, the norm runs in fp32 like ``F.rms_norm`` (which upcasts reduced-precision
+inputs and, for ``eps=None``, adds float32's epsilon), and the scale is one fp32 multiply
+rounded to the storage dtype. The order of the fp32 sum of squares is the only difference from
+the unfused ops: results agree within one unit in the last place of the storage dtype.
+"""
+from __future__ import annotations
+
+import torch
+
+from modelcore_amd import _ext
+
+__all__ = ["rope_norm_scale_append", "default_eps"]
+
+
+def default_eps() -> float:
+    """The epsilon ``F.rms_norm(x, eps=None)`` adds: float32's, for fp32 and reduced-precision
+    inputs alike (the computation is upcast to fp32 before the epsilon is chosen)."""
+    return float(torch.finfo(torch.float32).eps)
+
+
+def _table(t: torch.Tensor, half: int, dt: torch.dtype, device) -> torch.Tensor:
+    if t.dtype != dt:
+        raise TypeError(f"rotary table is {t.dtype}, q is {dt}")
+    if t.device != device:
+        raise ValueError(f"rotary table is on {t.device}, q on {device}")
+    if t.shape[-1] != half or t.numel() % half != 0:
+        raise ValueError(f"rotary table must end in head_dim/2 = {half}; got {tuple(t.shape)}")
+    return t.reshape(-1, half).contiguous()
+
+
+def rope_norm_scale_append(q, cos, sin, cache_seqlens, k=None, v=None, k_cache=None,
+                           v_cache=None, eps=None, scale=1.2):
+    """RoPE + RMS-norm + scale of q (returned) and, when given, of k, which is appended with v.
+
+    Args:
+        q: (B, T, H, D) queries, bf16 or fp32.
+        cos, sin: rotary tables that reshape to (n_pos, D/2) in q's dtype -- the
+            (1, n_pos, 1, D/2) buffers of the rotary module.
+        cache_seqlens: (B,) int32, each row's position before these tokens (read only).
+        k, v: (B, T, H_kv, D) new keys/values, or both None (transform q only).
+        k_cache, v_cache: (B, T_max, H_kv, D) caches (a slot view), updated in place at
+            cache_seqlens[b] + t.
+        eps: RMS-norm epsilon; None is ``F.rms_norm``'s default (see ``default_eps``).
+        scale: multiplier after the norm (1.2 in the model).
+    """
+    _ext.require_rocm(q, k, v, k_cache, v_cache, cache_seqlens, what="rope_norm_scale_append")
+    if q.dim() != 4:
+        raise ValueError(f"q must be (B, T, H, D); got {tuple(q.shape)}")
+    B, T, H, D = q.shape
+    if D % 2:
+        raise ValueError(f"head_dim must be even for RoPE; got {D}")
+    dt = q.dtype
+    code = _ext.dtype_code(dt)
+    half = D // 2
+    cos_t, sin_t = _table(cos, half, dt, q.device), _table(sin, half, dt, q.device)
+    if cos_t.shape != sin_t.shape:
+        raise ValueError(f"cos {tuple(cos_t.shape)} and sin {tuple(sin_t.shape)} differ")
+    if (k is None) != (v is None):
+        raise ValueError("pass both k and v, or neither")
+    seqlens = cache_seqlens
+    if seqlens.dtype != torch.int32 or seqlens.shape != (B,) or seqlens.device != q.device:
+        raise ValueError(f"cache_seqlens must be ({B},) int32 on {q.device}")
+    seqlens = seqlens.contiguous()
+    H_kv, T_max, cb = 1, 0, 0
+    if k is not None:
+        if k.dim() != 4 or k.shape != v.shape or k.shape[0] != B or k.shape[1] != T \
+                or k.shape[3] != D:
+            raise ValueError(f"k/v must be (B, T, H_kv, D) = ({B}, {T}, H_kv, {D}); got "
+                             f"{tuple(k.shape)} and {tuple(v.shape)}")
+        H_kv = k.shape[2]
+        if H % H_kv:
+            raise ValueError(f"n_head {H} is not a multiple of n_kv_head {H_kv}")
+        if k_cache is None or v_cache is None or k_cache.shape != v_cache.shape \
+                or k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[2:] != (H_kv, D):
+            raise ValueError(f"k_cache/v_cache must be (B, T_max, H_kv, D) = ({B}, T_max, {H_kv}, "
+                             f"{D})")
+        for name, t in (("k", k), ("v", v), ("k_cache", k_cache), ("v_cache", v_cache)):
+            if t.dtype != dt:
+                raise TypeError(f"{name} is {t.dtype}, q is {dt}")
+        if k_cache.stride() != v_cache.stride() or not k_cache[0].is_contiguous() \
+                or not v_cache[0].is_contiguous():
+            raise ValueError("each row of k_cache/v_cache must be contiguous (T_max, H_kv, D), "
+                             "with equal strides")
+        T_max, cb = k_cache.shape[1], k_cache.stride(0)
+        k, v = k.contiguous(), v.contiguous()
+    q = q.contiguous()
+    out = torch.empty_like(q)
+    eps = default_eps() if eps is None else float(eps)
+    st = _ext.lib().mcamd_qk_rope_norm_append(
+        q.data_ptr(), k.data_ptr() if k is not None else None,
+        v.data_ptr() if v is not None else None, cos_t.data_ptr(), sin_t.data_ptr(),
+        cos_t.shape[0], k_cache.data_ptr() if k is not None else None,
+        v_cache.data_ptr() if k is not None else None, seqlens.data_ptr(), out.data_ptr(), B, T,
+        H, H_kv, D, T_max, cb, eps, float(scale), code, _ext.stream_handle(q.device))
+    _ext.check(st, "rope_norm_scale_append")
+    return out

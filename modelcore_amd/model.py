@@ -182,6 +182,19 @@ class Rotary(nn.Module):
         return (self.cos[0].index_select(0, flat).view(B, T, 1, -1),
                 self.sin[0].index_select(0, flat).view(B, T, 1, -1))
 
+    def check_positions(self, T, kv_cache):
+        """The position asserts of _cos_sin without building the windows, for the fused path
+        that reads positions on the device: free when the cache is uniform, one host read when it
+        is ragged (as in the reference, modelcore/components/rotary.py:50-62)."""
+        pos = kv_cache.uniform_pos()
+        if pos is not None:
+            assert pos + T <= self.cos.size(1), \
+                f"Sequence length grew beyond the rotary embeddings cache: {pos + T} > {self.cos.size(1)}"
+            return
+        last = int(kv_cache.cache_seqlens.max().item()) + T - 1
+        assert last < self.cos.size(1), \
+            f"Sequence length grew beyond the rotary embeddings cache: {last + 1} > {self.cos.size(1)}"
+
     def forward(self, q, k, kv_cache):
         cos, sin = self._cos_sin(q.size(1), kv_cache)
         return rotate(q, cos, sin), rotate(k, cos, sin)
@@ -229,7 +242,7 @@ class Attention(nn.Module):
     passes them to the operator, which rewrites identical values at the same positions."""
 
     def __init__(self, n_embd, n_head, n_kv_head, head_dim, window, kv_slot, produces_kv,
-                 features, rope, norm, attention):
+                 features, rope, norm, attention, epilogue=None):
         super().__init__()
         if head_dim is None:
             assert n_embd % n_head == 0
@@ -243,6 +256,10 @@ class Attention(nn.Module):
         self.kv_slot = kv_slot
         self.produces_kv = produces_kv
         self.rope, self.norm, self.attention = rope, norm, attention
+        # RoPE + QK-norm + x1.2 + append in one launch (modelcore_amd.kernels.qk_epilogue) when
+        # decoding with a cache; None, or fuse_epilogue = False, runs the reference's separate ops.
+        self.epilogue = epilogue
+        self.fuse_epilogue = True
         self.c_q = Linear(n_embd, n_head * head_dim, bias=False)
         self.c_k = Linear(n_embd, n_kv_head * head_dim, bias=False) if produces_kv else None
         self.c_v = Linear(n_embd, n_kv_head * head_dim, bias=False) if produces_kv else None
@@ -275,6 +292,9 @@ class Attention(nn.Module):
     def forward(self, x, kv_cache, kv_bus):
         B, T, _ = x.size()
         q = self.c_q(x).view(B, T, self.n_head, self.head_dim)
+        if kv_cache is not None and self.epilogue is not None and self.fuse_epilogue \
+                and isinstance(self.norm, RMSNorm):
+            return self._forward_fused(x, q, kv_cache, kv_bus)
         if self.produces_kv:
             k = self.c_k(x).view(B, T, self.n_kv_head, self.head_dim)
             v = self.c_v(x).view(B, T, self.n_kv_head, self.head_dim)
@@ -293,6 +313,30 @@ class Attention(nn.Module):
             y = self.attention.flash_attn_with_kvcache(q, k_cache, v_cache, k=k, v=v,
                                                        cache_seqlens=kv_cache.cache_seqlens,
                                                        causal=True, window_size=window_size)
+        if "output_gate" in self.features:
+            y = self.features["output_gate"](y, x)
+        return self.c_proj(y.contiguous().view(B, T, -1))
+
+    def _forward_fused(self, x, q, kv_cache, kv_bus):
+        """The same layer with the pre-attention ops fused: a producer rotates, norms and scales
+        q and k and appends k, v to its slot in one launch; a KV-sharing consumer finds them there
+        already (the reference's consumer re-appends identical values, attention.py:70-80), so it
+        transforms q only. Then the operator runs without an append."""
+        B, T, _ = x.size()
+        self.rope.check_positions(T, kv_cache)
+        k_cache, v_cache = kv_cache.get_slot_cache(self.kv_slot)
+        seqlens = kv_cache.cache_seqlens
+        if self.produces_kv:
+            k = self.c_k(x).view(B, T, self.n_kv_head, self.head_dim)
+            v = self.c_v(x).view(B, T, self.n_kv_head, self.head_dim)
+            q = self.epilogue(q, self.rope.cos, self.rope.sin, seqlens, k, v, k_cache, v_cache,
+                              eps=self.norm.eps, scale=1.2)
+            kv_bus[self.kv_slot] = None  # consumers read the slot itself
+        else:
+            q = self.epilogue(q, self.rope.cos, self.rope.sin, seqlens, eps=self.norm.eps,
+                              scale=1.2)
+        y = self.attention.flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=seqlens,
+                                                   causal=True, window_size=(self.window, 0))
         if "output_gate" in self.features:
             y = self.features["output_gate"](y, x)
         return self.c_proj(y.contiguous().view(B, T, -1))
@@ -434,15 +478,23 @@ def _default_attention():
     return flash_attn
 
 
+def _default_epilogue():
+    from modelcore_amd.kernels.qk_epilogue import rope_norm_scale_append
+    return rope_norm_scale_append
+
+
 class Model(nn.Module):
     """Embedding -> blocks -> lm_head; advances the cache once per forward, after every layer
     (modelcore/model.py:93-101)."""
 
-    def __init__(self, config: ModelConfig, runtime: Runtime | None = None, attention=None):
+    def __init__(self, config: ModelConfig, runtime: Runtime | None = None, attention=None,
+                 epilogue=None):
         super().__init__()
         self.config = config
         self.runtime = runtime or Runtime()
-        attention = attention or _default_attention()
+        if attention is None:  # the native operator, and with it the fused pre-attention step
+            attention = _default_attention()
+            epilogue = epilogue or _default_epilogue()
         shared = {}
         for name, spec in config.shared.items():
             if spec.type == "rotary":
@@ -475,7 +527,7 @@ class Model(nn.Module):
             mixer = Attention(config.n_embd, mp["n_head"], mp.get("n_kv_head", mp["n_head"]),
                               mp.get("head_dim"), mp.get("window", -1), mp.get("kv_slot"),
                               mp.get("produces_kv", True), mp.get("features"), rope, norm,
-                              attention)
+                              attention, epilogue)
             f = p["ffn"]
             ffn_cls = {"gated_mlp": GatedMLP, "mlp": MLP}[f.type]
             ffn = ffn_cls(config.n_embd, f.params["activation"], f.params["hidden_dim"])
@@ -513,6 +565,13 @@ class Model(nn.Module):
             if isinstance(m, Linear):
                 m._cast = None
 
+    def set_fused_epilogue(self, enabled: bool):
+        """Choose, for every attention layer at once, between the fused pre-attention launch
+        (RoPE + QK-norm + x1.2 + append; the default with the native operator) and the
+        reference's separate ops. Results agree within one unit in the last place."""
+        for b in self.body.blocks:
+            b.mixer.fuse_epilogue = bool(enabled)
+
     def layer_specs(self):
         return [b.mixer.layer_spec() for b in self.body.blocks]
 
@@ -546,15 +605,17 @@ def kv_cache_spec(layer_specs):
 class ModelManager:
     """create_model / new_kv_cache / new_decoder (modelcore/manager.py:111-119, :286-299)."""
 
-    def __init__(self, runtime: Runtime | None = None, attention=None):
+    def __init__(self, runtime: Runtime | None = None, attention=None, epilogue=None):
         self.runtime = runtime or Runtime()
         self.attention = attention
+        self.epilogue = epilogue
 
     def create_model(self, config, *, device, seed=None):
         if isinstance(config, dict):
             config = ModelConfig.from_dict(config)
         with torch.device("meta"):
-            model = Model(config, runtime=self.runtime, attention=self.attention)
+            model = Model(config, runtime=self.runtime, attention=self.attention,
+                          epilogue=self.epilogue)
         model.to_empty(device=device)
         if seed is not None:
             torch.manual_seed(seed)

@@ -78,3 +78,22 @@ def test_a_missing_library_raises_with_its_reason(monkeypatch, tmp_path):
         monkeypatch.undo()
         _ext.reload()
     _ext.lib()
+
+
+def test_epilogue_rejects_odd_head_dim_half_kv_and_bad_dtype():
+    lib = _ext.lib()
+    fake = 1 << 20  # never dereferenced: the checks fail first
+    args = dict(n_pos=64, batch=2, t_new=1, n_head=8, n_kv_head=2, t_max=64, cb=64 * 2 * 128)
+
+    def call(k, v, head_dim, dtype):
+        return lib.mcamd_qk_rope_norm_append(fake, k, v, fake, fake, args["n_pos"], fake, fake,
+                                             fake, fake, args["batch"], args["t_new"],
+                                             args["n_head"], args["n_kv_head"], head_dim,
+                                             args["t_max"], args["cb"], 1e-6, 1.2, dtype, None)
+
+    assert call(fake, fake, 127, _ext.BF16) == _ext.EUNSUPPORTED
+    assert b"even" in lib.mcamd_last_error()
+    assert call(fake, None, 128, _ext.BF16) == _ext.EINVAL
+    assert b"both k and v" in lib.mcamd_last_error()
+    assert call(fake, fake, 128, 9) == _ext.EINVAL
+    assert b"dtype" in lib.mcamd_last_error()

@@ -206,3 +206,34 @@ def test_cached_inference_weights_give_identical_logits():
         b = model(idx)
         model.drop_inference_weights()
     assert torch.equal(a, b)
+
+
+def test_fused_pre_attention_step_matches_the_separate_ops():
+    """The same bf16 mixed-window, KV-sharing stack with the fused RoPE + QK-norm + x1.2 + append
+    launch (the default) and with the reference's separate ops, fed the same tokens (a prefill,
+    then cached single-token steps): caches and logits agree within bf16 rounding."""
+    _note("fused vs separate pre-attention step")
+    cfg = mixed_window_config()
+    mgr = gpu_manager(torch.bfloat16)
+    model = awake(mgr.create_model(cfg, device=DEV, seed=0))
+    g = torch.Generator().manual_seed(4)
+    B, P, steps = 3, 120, 8
+    tokens = torch.randint(0, cfg.vocab_size, (B, P + steps), generator=g).to(DEV)
+    runs = []
+    for fused in (True, False):
+        model.set_fused_epilogue(fused)
+        cache = mgr.new_kv_cache(model, batch_size=B, seq_len=P + steps)
+        with torch.no_grad():
+            logits = [model(tokens[:, :P], kv_cache=cache)[:, -1]]
+            for t in range(P, P + steps):
+                logits.append(model(tokens[:, t:t + 1], kv_cache=cache)[:, -1])
+        runs.append((torch.stack(logits).float(), cache))
+    model.set_fused_epilogue(True)
+    (la, ca), (lb, cb) = runs
+    err = (la - lb).abs().max().item()
+    print(f"logits max-abs fused vs separate: {err:.4f} (scale {lb.abs().max().item():.3f})",
+          flush=True)
+    assert err <= 0.1
+    assert torch.equal(ca.cache_seqlens, cb.cache_seqlens)
+    for a, b in ((ca.k_cache, cb.k_cache), (ca.v_cache, cb.v_cache)):
+        assert (a.float() - b.float()).abs().max() <= 0.1
