@@ -407,14 +407,24 @@ def bench_sample(args):
     torch.cuda.synchronize()
     prefill_ms = start.elapsed_time(end)
     sampler = PhiloxSampler(SM_ROWS, dev, base_seed=0)
-    log(f"prefill + replicate {prefill_ms:.1f} ms; decoding {W} + {K} steps")
+    graph = not args.eager
+    if graph and W == 0:  # capturing runs one real step first
+        W, K = 1, SM_NEW - 1
+    log(f"prefill + replicate {prefill_ms:.1f} ms; decoding {W} + {K} steps "
+        f"({'one captured graph per step' if graph else 'eager'})")
     with torch.inference_mode():
-        for _ in range(W):
-            dec.step(sampler(dec.logits, 1.0).view(-1))
+        if graph:
+            step = dec.capture(sampler, 1.0)  # includes the first warm-up step
+            for _ in range(W - 1):
+                step()
+        else:
+            step = lambda: dec.step(sampler(dec.logits, 1.0).view(-1))  # noqa: E731
+            for _ in range(W):
+                step()
         torch.cuda.synchronize()
         start.record()
         for _ in range(K):
-            dec.step(sampler(dec.logits, 1.0).view(-1))
+            step()
         end.record()
         torch.cuda.synchronize()
     ms = start.elapsed_time(end) / K
@@ -432,7 +442,8 @@ def bench_sample(args):
         "warmup": W, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "batch-1 prefill of 2048 tokens, KVCache.prefill to 64 rows, "
-                               "then one model forward + device sampling per step",
+                               "then one model forward + device sampling per step"
+                               + (" (the step captured once as a HIP graph)" if graph else ""),
                    "layers": SM_LAYERS, "d_model": SM_D, "n_head": SM_H, "n_kv_head": SM_HKV,
                    "head_dim": D, "mlp_hidden": SM_HID, "vocab": SM_V, "rows": SM_ROWS,
                    "prompt": SM_PROMPT, "new_tokens": SM_NEW,

@@ -142,7 +142,9 @@ int mcamd_sample_tokens(const float *logits, int64_t batch, int64_t vocab, int64
 /*
  * The step before the operator, fused: RoPE at each token's position p = cache_seqlens[b] + t,
  * RMS-norm over head_dim (eps added to the mean square, fp32 arithmetic), and `scale`, applied to
- * q (written to q_out, (batch, t_new, n_head, head_dim)) and to k, which is then appended with v
+ * q (written to q_out, (batch, t_new, n_head, head_dim) contiguous) and to k, which is then
+ * appended with v. q, k, v are (batch, t_new, heads, head_dim) with heads contiguous and tokens
+ * `*_token_stride` elements apart (the views of a fused QKV projection); k is appended with v
  * at p as mcamd_kv_append does. `cos`/`sin` are the rotary tables, (n_pos, head_dim / 2) in the
  * storage dtype. k = v = NULL transforms q only (k_cache/v_cache unused). Each rotation product
  * and sum is rounded to the storage dtype like the separate torch ops; only the order of the
@@ -153,12 +155,25 @@ int mcamd_sample_tokens(const float *logits, int64_t batch, int64_t vocab, int64
  * multiplies, and the append half of flash_attn_with_kvcache (modelcore/kernels/flash_attn.py:
  * 336-346). Positions come from cache_seqlens on the device: no host sync.
  */
-int mcamd_qk_rope_norm_append(const void *q, const void *k, const void *v, const void *cos,
-                              const void *sin, int64_t n_pos, void *k_cache, void *v_cache,
+int mcamd_qk_rope_norm_append(const void *q, int64_t q_token_stride, const void *k,
+                              int64_t k_token_stride, const void *v, int64_t v_token_stride,
+                              const void *cos, const void *sin, int64_t n_pos, void *k_cache,
+                              void *v_cache,
                               const int32_t *cache_seqlens, void *q_out, int64_t batch,
                               int64_t t_new, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
                               int64_t t_max, int64_t cache_batch_stride, float eps, float scale,
                               int dtype, void *stream);
+
+/*
+ * y = x . W^T for decode-sized batches: x (m, k) bf16 rows `ldx` elements apart, m <= 64; W
+ * (n, k) bf16 contiguous (the nn.Linear weight layout); y (m, n) bf16 rows `ldy` apart; fp32
+ * accumulation in a fixed order (deterministic). n must be a multiple of 32 and k of 512;
+ * rows_per_group (32 or 64) is the number of W rows one workgroup streams.
+ * Replaces F.linear in Linear.forward (modelcore/components/linear.py:13-14) for the projections
+ * of a decode step, where reading the weights once from HBM is the whole cost.
+ */
+int mcamd_linear_bf16(const void *x, int64_t ldx, const void *w, void *y, int64_t ldy, int64_t m,
+                      int64_t n, int64_t k, int rows_per_group, void *stream);
 
 #ifdef __cplusplus
 }

@@ -21,7 +21,7 @@ LIB_PATH = Path(os.environ.get("MODELCORE_AMD_LIB",
 # Element-type and status codes of the C ABI.
 F32, BF16 = 0, 1
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH = 0, -1, -2, -3, -4
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -46,9 +46,11 @@ SIGNATURES = {
                                        _i64, _i64, _i64, _i64, _int, _ptr]),
     "mcamd_sample_tokens": (_int, [_ptr, _i64, _i64, _i64, ctypes.c_float, _ptr, _ptr, _ptr,
                                    _ptr]),
-    "mcamd_qk_rope_norm_append": (_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _ptr,
-                                         _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                                         ctypes.c_float, ctypes.c_float, _int, _ptr]),
+    "mcamd_qk_rope_norm_append": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _i64,
+                                         _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64,
+                                         _i64, _i64, ctypes.c_float, ctypes.c_float, _int,
+                                         _ptr]),
+    "mcamd_linear_bf16": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _int, _ptr]),
 }
 
 _LIB = None

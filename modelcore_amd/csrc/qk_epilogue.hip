@@ -12,7 +12,9 @@
 //   norm  (modelcore/components/norm.py:43-44, F.rms_norm without weight): in fp32,
 //           z = y * (1 / sqrt(mean(y^2) + eps)), rounded to the storage dtype;
 //   scale: out = z * scale (1.2 in the model) in fp32, rounded to the storage dtype.
-// q's result goes to q_out; k's result and v (unchanged) go to k_cache / v_cache at p
+// q, k and v may be strided views (a fused QKV projection's output): tokens are `*_token_stride`
+// elements apart, heads contiguous within a token. q's result goes to q_out (contiguous); k's
+// result and v (unchanged) go to k_cache / v_cache at p
 // (modelcore/kernels/flash_attn.py:336-346). With k = v = null only q is transformed: the
 // KV-sharing consumer layers (attention.py:152-157).
 //
@@ -66,6 +68,7 @@ struct EpiParams {
   void *k_cache, *v_cache, *q_out;
   const int32_t *seqlens;
   int64_t n_tokens, n_pos, t_max, cache_b;
+  int64_t q_tok, k_tok, v_tok;  // elements between consecutive tokens of q, k, v
   int t_new, H, H_kv, D, n_items;
   float eps, scale;
 };
@@ -92,14 +95,14 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void qk_epilogue_kernel(EpiPar
   if (item >= P.H + P.H_kv) {  // v: plain copy into the cache
     if (!in_cache) return;
     const int hk = item - P.H - P.H_kv;
-    const T *src = static_cast<const T *>(P.v) + (tok * P.H_kv + hk) * P.D;
+    const T *src = static_cast<const T *>(P.v) + tok * P.v_tok + int64_t(hk) * P.D;
     T *dst = static_cast<T *>(P.v_cache) + int64_t(b) * P.cache_b + (pos * P.H_kv + hk) * P.D;
     for (int d = lane; d < P.D; d += 64) dst[d] = src[d];
     return;
   }
   const bool is_q = item < P.H;
-  const T *src = is_q ? static_cast<const T *>(P.q) + (tok * P.H + item) * P.D
-                      : static_cast<const T *>(P.k) + (tok * P.H_kv + (item - P.H)) * P.D;
+  const T *src = is_q ? static_cast<const T *>(P.q) + tok * P.q_tok + int64_t(item) * P.D
+                      : static_cast<const T *>(P.k) + tok * P.k_tok + int64_t(item - P.H) * P.D;
   T *dst;
   if (is_q) {
     dst = static_cast<T *>(P.q_out) + (tok * P.H + item) * P.D;
@@ -147,8 +150,10 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void qk_epilogue_kernel(EpiPar
 
 using namespace mcamd;
 
-extern "C" int mcamd_qk_rope_norm_append(const void *q, const void *k, const void *v,
-                                         const void *cos, const void *sin, int64_t n_pos,
+extern "C" int mcamd_qk_rope_norm_append(const void *q, int64_t q_token_stride, const void *k,
+                                         int64_t k_token_stride, const void *v,
+                                         int64_t v_token_stride, const void *cos,
+                                         const void *sin, int64_t n_pos,
                                          void *k_cache, void *v_cache,
                                          const int32_t *cache_seqlens, void *q_out,
                                          int64_t batch, int64_t t_new, int64_t n_head,
@@ -175,6 +180,9 @@ extern "C" int mcamd_qk_rope_norm_append(const void *q, const void *k, const voi
     return fail(MCAMD_EINVAL, "qk_rope_norm_append: null pointer or empty cache");
   if (with_kv && cache_batch_stride < t_max * n_kv_head * head_dim)
     return fail(MCAMD_EINVAL, "qk_rope_norm_append: cache_batch_stride smaller than T_max*H_kv*D");
+  if (q_token_stride < n_head * head_dim ||
+      (with_kv && (k_token_stride < n_kv_head * head_dim || v_token_stride < n_kv_head * head_dim)))
+    return fail(MCAMD_EINVAL, "qk_rope_norm_append: a token stride is smaller than heads * head_dim");
   EpiParams P;
   P.q = q;
   P.k = k;
@@ -184,6 +192,9 @@ extern "C" int mcamd_qk_rope_norm_append(const void *q, const void *k, const voi
   P.k_cache = k_cache;
   P.v_cache = v_cache;
   P.q_out = q_out;
+  P.q_tok = q_token_stride;
+  P.k_tok = k_token_stride;
+  P.v_tok = v_token_stride;
   P.seqlens = cache_seqlens;
   P.n_tokens = batch * t_new;
   P.n_pos = n_pos;

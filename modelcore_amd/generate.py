@@ -76,3 +76,70 @@ class Decoder:
             ids = torch.tensor(token_column, dtype=torch.long, device=device).unsqueeze(1)
         self._logits = self.model.forward(ids, kv_cache=self.kv_cache)[:, -1, :]
         return self._logits
+
+    def capture(self, sampler, temperature=1.0):
+        """A ``CapturedStep`` of this decoder: each call samples from the current logits on the
+        device and steps every row, as one graph replay."""
+        return CapturedStep(self, sampler, temperature)
+
+
+class CapturedStep:
+    """One whole decode step -- model forward on every row's last token, device sampling of the
+    next token, cache advance -- recorded once as a HIP graph and replayed per position.
+
+    The reference's step (modelcore/generate.py:82-94) returns to the host between positions: it
+    builds the token column from a Python list and samples with torch.multinomial. Here the
+    tokens stay on the device: the sampled column is written into the buffer the next replay
+    reads, so a replay is one graph launch with no host sync. What the graph cannot do -- move the
+    cache's host-side position and check it against the rotary table and the cache length -- runs
+    on the host around each replay, without touching the device.
+
+    Needs a uniform cache (every row at one position, as after ``KVCache.prefill``): a ragged
+    cache checks its rotary positions with a device read, which a graph cannot hold. The first
+    column is drawn from the decoder's current logits when the step is built, and building runs
+    one real step (the warm-up that settles lazily created buffers) before the capture.
+    """
+
+    @torch.inference_mode()
+    def __init__(self, decoder, sampler, temperature=1.0):
+        self.decoder, self.sampler, self.temperature = decoder, sampler, float(temperature)
+        cache = decoder.kv_cache
+        if cache.uniform_pos() is None:
+            raise ValueError("CapturedStep needs a uniform cache (rows at one position)")
+        model = decoder.model
+        self._rotary_len = min(b.mixer.rope.cos.size(1) for b in model.body.blocks)
+        self.tokens = sampler(decoder.logits, self.temperature).view(-1, 1).clone()
+        side = torch.cuda.Stream(device=self.tokens.device)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self._check()
+            self._body()  # warm-up: a real step
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        pos = cache._pos_uniform
+        self._check()
+        with torch.cuda.graph(self.graph, stream=side):
+            self._body()
+        cache._pos_uniform = pos  # the capture ran no kernel: the cache did not move
+        torch.cuda.current_stream().wait_stream(side)
+
+    def _check(self):
+        cache = self.decoder.kv_cache
+        pos = cache.uniform_pos()
+        assert pos + 1 <= self._rotary_len, \
+            f"Sequence length grew beyond the rotary embeddings cache: {pos + 1} > {self._rotary_len}"
+        assert pos + 1 <= cache.max_seq_len, \
+            f"Sequence length {pos + 1} exceeds cache length {cache.max_seq_len}"
+
+    def _body(self):
+        logits = self.decoder.model.forward(self.tokens, kv_cache=self.decoder.kv_cache)[:, -1, :]
+        self.decoder._logits = logits
+        self.tokens.copy_(self.sampler(logits, self.temperature).view(-1, 1))
+
+    def __call__(self):
+        """Feed the current token column, sample the next into ``self.tokens`` (returned; it is
+        overwritten by the next call), advance every row one position."""
+        self._check()
+        self.graph.replay()
+        self.decoder.kv_cache._pos_uniform += 1
+        return self.tokens

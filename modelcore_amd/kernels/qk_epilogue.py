@@ -44,12 +44,24 @@ def _table(t: torch.Tensor, half: int, dt: torch.dtype, device) -> torch.Tensor:
     return t.reshape(-1, half).contiguous()
 
 
+def _token_rows(t: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """t (B, T, heads, D) with heads and D contiguous and tokens evenly strided (a view of a fused
+    projection's output qualifies), and the token stride in elements; else a contiguous copy."""
+    B, T, Hh, D = t.shape
+    if t.stride(3) == 1 and t.stride(2) == D and t.stride(0) == T * t.stride(1) \
+            and t.stride(1) >= Hh * D:
+        return t, t.stride(1)
+    t = t.contiguous()
+    return t, Hh * D
+
+
 def rope_norm_scale_append(q, cos, sin, cache_seqlens, k=None, v=None, k_cache=None,
                            v_cache=None, eps=None, scale=1.2):
     """RoPE + RMS-norm + scale of q (returned) and, when given, of k, which is appended with v.
 
     Args:
-        q: (B, T, H, D) queries, bf16 or fp32.
+        q: (B, T, H, D) queries, bf16 or fp32; q, k and v may be strided views of one fused
+            projection (heads contiguous, tokens evenly strided), read in place.
         cos, sin: rotary tables that reshape to (n_pos, D/2) in q's dtype -- the
             (1, n_pos, 1, D/2) buffers of the rotary module.
         cache_seqlens: (B,) int32, each row's position before these tokens (read only).
@@ -98,13 +110,15 @@ def rope_norm_scale_append(q, cos, sin, cache_seqlens, k=None, v=None, k_cache=N
             raise ValueError("each row of k_cache/v_cache must be contiguous (T_max, H_kv, D), "
                              "with equal strides")
         T_max, cb = k_cache.shape[1], k_cache.stride(0)
-        k, v = k.contiguous(), v.contiguous()
-    q = q.contiguous()
-    out = torch.empty_like(q)
+        (k, ks), (v, vs) = _token_rows(k), _token_rows(v)
+    else:
+        ks = vs = 0
+    q, qs = _token_rows(q)
+    out = torch.empty((B, T, H, D), dtype=dt, device=q.device)
     eps = default_eps() if eps is None else float(eps)
     st = _ext.lib().mcamd_qk_rope_norm_append(
-        q.data_ptr(), k.data_ptr() if k is not None else None,
-        v.data_ptr() if v is not None else None, cos_t.data_ptr(), sin_t.data_ptr(),
+        q.data_ptr(), qs, k.data_ptr() if k is not None else None, ks,
+        v.data_ptr() if v is not None else None, vs, cos_t.data_ptr(), sin_t.data_ptr(),
         cos_t.shape[0], k_cache.data_ptr() if k is not None else None,
         v_cache.data_ptr() if k is not None else None, seqlens.data_ptr(), out.data_ptr(), B, T,
         H, H_kv, D, T_max, cb, eps, float(scale), code, _ext.stream_handle(q.device))

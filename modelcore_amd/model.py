@@ -260,6 +260,7 @@ class Attention(nn.Module):
         # decoding with a cache; None, or fuse_epilogue = False, runs the reference's separate ops.
         self.epilogue = epilogue
         self.fuse_epilogue = True
+        self._qkv = None  # [W_q; W_k; W_v] in the compute dtype, set by cache_inference_weights
         self.c_q = Linear(n_embd, n_head * head_dim, bias=False)
         self.c_k = Linear(n_embd, n_kv_head * head_dim, bias=False) if produces_kv else None
         self.c_v = Linear(n_embd, n_kv_head * head_dim, bias=False) if produces_kv else None
@@ -289,15 +290,31 @@ class Attention(nn.Module):
         return AttentionLayerSpec(self.n_head, self.n_kv_head, self.head_dim, self.window,
                                   self.kv_slot)
 
+    def _project(self, x):
+        """q, k, v (k = v = None for a consumer layer) as (B, T, heads, D) views; one product
+        against the stacked [W_q; W_k; W_v] when the inference weights are cached (the same dot
+        products as three separate ones, read in one pass over the weights)."""
+        B, T, _ = x.size()
+        Hq, Hk, D = self.n_head * self.head_dim, self.n_kv_head * self.head_dim, self.head_dim
+        if self._qkv is not None and self._qkv.dtype == x.dtype:
+            qkv = F.linear(x, self._qkv)
+            q = qkv[..., :Hq].view(B, T, self.n_head, D)
+            k = qkv[..., Hq:Hq + Hk].view(B, T, self.n_kv_head, D)
+            v = qkv[..., Hq + Hk:].view(B, T, self.n_kv_head, D)
+            return q, k, v
+        q = self.c_q(x).view(B, T, self.n_head, D)
+        if not self.produces_kv:
+            return q, None, None
+        return (q, self.c_k(x).view(B, T, self.n_kv_head, D),
+                self.c_v(x).view(B, T, self.n_kv_head, D))
+
     def forward(self, x, kv_cache, kv_bus):
         B, T, _ = x.size()
-        q = self.c_q(x).view(B, T, self.n_head, self.head_dim)
+        q, k, v = self._project(x)
         if kv_cache is not None and self.epilogue is not None and self.fuse_epilogue \
                 and isinstance(self.norm, RMSNorm):
-            return self._forward_fused(x, q, kv_cache, kv_bus)
+            return self._forward_fused(x, q, k, v, kv_cache, kv_bus)
         if self.produces_kv:
-            k = self.c_k(x).view(B, T, self.n_kv_head, self.head_dim)
-            v = self.c_v(x).view(B, T, self.n_kv_head, self.head_dim)
             q, k = self.rope(q, k, kv_cache)
             q, k = self.norm(q), self.norm(k)
             q, k = q * 1.2, k * 1.2
@@ -317,7 +334,7 @@ class Attention(nn.Module):
             y = self.features["output_gate"](y, x)
         return self.c_proj(y.contiguous().view(B, T, -1))
 
-    def _forward_fused(self, x, q, kv_cache, kv_bus):
+    def _forward_fused(self, x, q, k, v, kv_cache, kv_bus):
         """The same layer with the pre-attention ops fused: a producer rotates, norms and scales
         q and k and appends k, v to its slot in one launch; a KV-sharing consumer finds them there
         already (the reference's consumer re-appends identical values, attention.py:70-80), so it
@@ -327,8 +344,6 @@ class Attention(nn.Module):
         k_cache, v_cache = kv_cache.get_slot_cache(self.kv_slot)
         seqlens = kv_cache.cache_seqlens
         if self.produces_kv:
-            k = self.c_k(x).view(B, T, self.n_kv_head, self.head_dim)
-            v = self.c_v(x).view(B, T, self.n_kv_head, self.head_dim)
             q = self.epilogue(q, self.rope.cos, self.rope.sin, seqlens, k, v, k_cache, v_cache,
                               eps=self.norm.eps, scale=1.2)
             kv_bus[self.kv_slot] = None  # consumers read the slot itself
@@ -356,6 +371,8 @@ class GatedMLP(nn.Module):
         self.gate_proj = Linear(n_embd, hidden_dim, bias=False)
         self.up_proj = Linear(n_embd, hidden_dim, bias=False)
         self.down_proj = Linear(hidden_dim, n_embd, bias=False)
+        self.hidden_dim = hidden_dim
+        self._gate_up = None  # [W_gate; W_up] in the compute dtype, set by cache_inference_weights
 
     @torch.no_grad()
     def init_weights(self):
@@ -365,6 +382,9 @@ class GatedMLP(nn.Module):
         nn.init.zeros_(self.down_proj.weight)
 
     def forward(self, x):
+        if self._gate_up is not None and self._gate_up.dtype == x.dtype:
+            gate, up = F.linear(x, self._gate_up).split(self.hidden_dim, dim=-1)
+            return self.down_proj(self.act(gate) * up)
         return self.down_proj(self.act(self.gate_proj(x)) * self.up_proj(x))
 
 
@@ -549,21 +569,40 @@ class Model(nn.Module):
         self.unembedding.init_weights()
 
     @torch.no_grad()
-    def cache_inference_weights(self, dtype=None):
+    def cache_inference_weights(self, dtype=None, fuse=True):
         """Keep a copy of every Linear weight in `dtype` (default: the compute dtype) and use it
-        instead of casting the fp32 master weight at every call. The products are bit-identical
-        (the cast is the same); the per-step weight traffic of a decode drops from a read of the
-        fp32 weights plus a write and a read of the cast copy to one read of the copy. Call again
+        instead of casting the fp32 master weight at every call: the per-step weight traffic of a
+        decode drops from a read of the fp32 weights plus a write and a read of the cast copy to
+        one read of the copy. With ``fuse=False`` the products are bit-identical to the uncached
+        ones (the cast is the same). With ``fuse`` (the default) the copies of W_q, W_k, W_v of
+        each KV-producing attention layer, and of W_gate, W_up of each gated MLP, are stacked so
+        one product reads each group in one pass -- the same dot products, which the library GEMM
+        may sum in another order (differences at the rounding of the compute dtype). Call again
         after the master weights change; ``drop_inference_weights`` undoes it."""
         dtype = dtype or self.runtime.compute_dtype
+        self.drop_inference_weights()
         for m in self.modules():
-            if isinstance(m, Linear):
+            if fuse and isinstance(m, Attention) and m.produces_kv:
+                stacked = torch.cat([m.c_q.weight, m.c_k.weight, m.c_v.weight]).to(dtype)
+                m._qkv = stacked
+                q, kv = m.c_q.out_features, m.c_k.out_features
+                m.c_q._cast, m.c_k._cast, m.c_v._cast = stacked.split([q, kv, kv])
+            elif fuse and isinstance(m, GatedMLP):
+                stacked = torch.cat([m.gate_proj.weight, m.up_proj.weight]).to(dtype)
+                m._gate_up = stacked
+                m.gate_proj._cast, m.up_proj._cast = stacked.split(m.hidden_dim)
+        for m in self.modules():
+            if isinstance(m, Linear) and m._cast is None:
                 m._cast = m.weight.detach().to(dtype)
 
     def drop_inference_weights(self):
         for m in self.modules():
             if isinstance(m, Linear):
                 m._cast = None
+            elif isinstance(m, Attention):
+                m._qkv = None
+            elif isinstance(m, GatedMLP):
+                m._gate_up = None
 
     def set_fused_epilogue(self, enabled: bool):
         """Choose, for every attention layer at once, between the fused pre-attention launch

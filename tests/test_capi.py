@@ -86,7 +86,8 @@ def test_epilogue_rejects_odd_head_dim_half_kv_and_bad_dtype():
     args = dict(n_pos=64, batch=2, t_new=1, n_head=8, n_kv_head=2, t_max=64, cb=64 * 2 * 128)
 
     def call(k, v, head_dim, dtype):
-        return lib.mcamd_qk_rope_norm_append(fake, k, v, fake, fake, args["n_pos"], fake, fake,
+        return lib.mcamd_qk_rope_norm_append(fake, 8 * head_dim, k, 2 * head_dim, v,
+                                             2 * head_dim, fake, fake, args["n_pos"], fake, fake,
                                              fake, fake, args["batch"], args["t_new"],
                                              args["n_head"], args["n_kv_head"], head_dim,
                                              args["t_max"], args["cb"], 1e-6, 1.2, dtype, None)
@@ -97,3 +98,7 @@ def test_epilogue_rejects_odd_head_dim_half_kv_and_bad_dtype():
     assert b"both k and v" in lib.mcamd_last_error()
     assert call(fake, fake, 128, 9) == _ext.EINVAL
     assert b"dtype" in lib.mcamd_last_error()
+    st = lib.mcamd_qk_rope_norm_append(fake, 100, fake, 256, fake, 256, fake, fake, 64, fake, fake,
+                                       fake, fake, 2, 1, 8, 2, 128, 64, 64 * 2 * 128, 1e-6, 1.2,
+                                       _ext.BF16, None)
+    assert st == _ext.EINVAL and b"token stride" in lib.mcamd_last_error()

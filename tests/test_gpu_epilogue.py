@@ -73,6 +73,26 @@ def test_fused_step_matches_the_separate_ops(dtype, D, H, H_kv, T, seqlens):
         assert torch.equal(gkc[b, keep].cpu(), c["kc"][b, keep])
 
 
+def test_strided_views_of_a_fused_projection_are_read_in_place():
+    _note("epilogue strided qkv")
+    dtype = torch.bfloat16
+    B, T, H, H_kv, D, T_max = 3, 5, 8, 2, 128, 32
+    c = _case(6, B, T, H, H_kv, D, T_max, T_max, dtype, [0, 4, 20])
+    qkv = torch.cat([c["q"].reshape(B, T, -1), c["k"].reshape(B, T, -1),
+                     c["v"].reshape(B, T, -1)], dim=-1).to(DEV)
+    q = qkv[..., :H * D].view(B, T, H, D)
+    k = qkv[..., H * D:(H + H_kv) * D].view(B, T, H_kv, D)
+    v = qkv[..., (H + H_kv) * D:].view(B, T, H_kv, D)
+    assert not q.is_contiguous()
+    dev = {n: c[n].to(DEV) for n in ("cos", "sin", "seqlens")}
+    kc1, vc1 = c["kc"].to(DEV), c["vc"].to(DEV)
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    a = rope_norm_scale_append(q, dev["cos"], dev["sin"], dev["seqlens"], k, v, kc1, vc1)
+    b = rope_norm_scale_append(q.contiguous(), dev["cos"], dev["sin"], dev["seqlens"],
+                               k.contiguous(), v.contiguous(), kc2, vc2)
+    assert torch.equal(a, b) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+
+
 def test_queries_only_for_kv_sharing_consumers():
     _note("epilogue q only")
     dtype = torch.bfloat16

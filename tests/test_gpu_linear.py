@@ -1,0 +1,80 @@
+"""The decode-sized bf16 product y = x . W^T (mcamd_linear_bf16) against float64 products of the
+same bf16 values (numpy), for the projection shapes of the decode workloads and edge sizes.
+
+Tolerance: the bf16 rounding of the output (2^-8 of |y|) plus fp32 accumulation, bounded by
+1e-5 of sum_k |x_k w_k|. The kernel sums its K-split partials in a fixed order, so two calls are
+bit-identical.
+"""
+import numpy as np
+import pytest
+import torch
+
+from modelcore_amd.kernels.linear import linear_bf16, supported
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+
+
+def _note(*a):
+    print("case:", *a, flush=True)
+
+
+def _check(y, x, w):
+    xd = x.float().cpu().double().numpy().reshape(-1, x.shape[-1])
+    wd = w.float().cpu().double().numpy()
+    ref = xd @ wd.T
+    bound = np.abs(xd) @ np.abs(wd).T
+    got = y.float().cpu().double().numpy().reshape(ref.shape)
+    err = np.abs(got - ref)
+    assert np.all(err <= np.abs(ref) * 2.0 ** -8 + 1e-5 * bound + 1e-30), float(err.max())
+
+
+SHAPES = [(1, 1024, 512), (7, 4096, 4096), (33, 1024, 1536), (64, 14336, 4096),
+          (64, 4096, 14336), (32, 6144, 4096), (64, 32768, 1024)]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_products_match_float64(m, n, k):
+    _note("linear", m, n, k)
+    g = torch.Generator().manual_seed(m + n + k)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(n, k, generator=g) * k ** -0.5).to(torch.bfloat16).to(DEV)
+    y = linear_bf16(x, w)
+    _check(y, x, w)
+    assert torch.equal(y, linear_bf16(x, w))  # deterministic
+
+
+@pytest.mark.parametrize("rpg", [32, 64])
+def test_both_workgroup_heights_give_the_same_bits(rpg, monkeypatch):
+    from modelcore_amd.kernels import linear as lin
+    _note("linear rows_per_group", rpg)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(40, 2048, generator=g).to(torch.bfloat16).to(DEV)
+    w = torch.randn(2048, 2048, generator=g).to(torch.bfloat16).to(DEV)
+    monkeypatch.setattr(lin, "_rows_per_group", lambda n: rpg)
+    y = linear_bf16(x, w)
+    _check(y, x, w)
+    monkeypatch.setattr(lin, "_rows_per_group", lambda n: 96 - rpg)
+    assert torch.equal(y, linear_bf16(x, w))  # same K split, same summation order
+
+
+def test_strided_rows_and_leading_dims():
+    _note("linear strided")
+    g = torch.Generator().manual_seed(10)
+    wide = torch.randn(3, 4, 1536, generator=g).to(torch.bfloat16).to(DEV)
+    x = wide[..., :1024]  # rows 1536 elements apart
+    w = torch.randn(512, 1024, generator=g).to(torch.bfloat16).to(DEV)
+    y = linear_bf16(x, w)
+    assert y.shape == (3, 4, 512)
+    _check(y, x, w)
+
+
+def test_unsupported_shapes_are_refused():
+    x = torch.zeros(65, 512, dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros(64, 512, dtype=torch.bfloat16, device=DEV)
+    assert not supported(x, w)
+    with pytest.raises(ValueError):
+        linear_bf16(x, w)
+    assert not supported(x[:8, :500], w[:, :500])  # k not a multiple of 512
+    assert not supported(x[:8].float(), w.float())

@@ -196,16 +196,25 @@ def test_sampling_decoder_rows_are_replicas_and_draws_are_reproducible():
 
 
 def test_cached_inference_weights_give_identical_logits():
+    """The bf16 weight copies give the logits of the per-call casts bit for bit; stacking the
+    QKV and gate/up copies into one product each changes only the GEMM's summation order."""
     cfg = mixed_window_config(n_layer=2)
     mgr = gpu_manager(torch.bfloat16)
     model = awake(mgr.create_model(cfg, device=DEV, seed=0))
     idx = torch.randint(0, cfg.vocab_size, (2, 40), generator=torch.Generator().manual_seed(3)).to(DEV)
     with torch.no_grad():
         a = model(idx)
-        model.cache_inference_weights()
+        model.cache_inference_weights(fuse=False)
         b = model(idx)
+        model.cache_inference_weights()
+        assert model.body.blocks[0].mixer._qkv is not None
+        c = model(idx)
         model.drop_inference_weights()
-    assert torch.equal(a, b)
+        d = model(idx)
+    assert torch.equal(a, b) and torch.equal(a, d)
+    err = (a.float() - c.float()).abs().max().item()
+    print(f"stacked projections: logits max-abs {err:.4f}", flush=True)
+    assert err <= 0.05
 
 
 def test_fused_pre_attention_step_matches_the_separate_ops():
@@ -237,3 +246,40 @@ def test_fused_pre_attention_step_matches_the_separate_ops():
     assert torch.equal(ca.cache_seqlens, cb.cache_seqlens)
     for a, b in ((ca.k_cache, cb.k_cache), (ca.v_cache, cb.v_cache)):
         assert (a.float() - b.float()).abs().max() <= 0.1
+
+
+def test_captured_decode_step_replays_the_eager_steps():
+    """A whole decode step (forward, device sampling, advance) captured once as a HIP graph and
+    replayed: the same tokens, logits and cache as the same steps run eagerly, and the host-side
+    position kept in step with the device."""
+    from modelcore_amd.sampling import PhiloxSampler
+    _note("captured decode step")
+    cfg = mixed_window_config(n_layer=4)
+    mgr = gpu_manager(torch.bfloat16)
+    model = awake(mgr.create_model(cfg, device=DEV, seed=0))
+    model.cache_inference_weights()
+    prompt = torch.randint(0, cfg.vocab_size, (90,), generator=torch.Generator().manual_seed(5))
+    R, n = 6, 10
+
+    eager = mgr.new_decoder(model, prompt.tolist(), num_samples=R, max_tokens=n + 2)
+    sampler = PhiloxSampler(R, DEV, base_seed=7)
+    toks, logits = [], []
+    for _ in range(n + 1):
+        t = sampler(eager.logits, 1.0).view(-1)
+        toks.append(t.clone())
+        eager.step(t)
+        logits.append(eager.logits.float().clone())
+
+    dec = mgr.new_decoder(model, prompt.tolist(), num_samples=R, max_tokens=n + 2)
+    step = dec.capture(PhiloxSampler(R, DEV, base_seed=7), 1.0)
+    assert torch.equal(step.tokens.view(-1), toks[1])  # the warm-up ran the first step
+    assert dec.kv_cache.get_pos() == 90 + 1
+    for i in range(1, n):
+        out = step()
+        assert dec.kv_cache.get_pos() == 90 + 1 + i
+        assert torch.equal(out.view(-1), toks[i + 1]), i
+        err = (dec.logits.float() - logits[i]).abs().max().item()
+        assert err <= 1e-2, (i, err)
+    torch.cuda.synchronize()
+    assert dec.kv_cache.cache_seqlens.tolist() == [90 + n] * R
+    assert torch.equal(dec.kv_cache.k_cache[:, :, :90 + n], eager.kv_cache.k_cache[:, :, :90 + n])
