@@ -67,8 +67,8 @@ class KVCache:
         if self._pos_uniform is not None:
             self._pos_uniform += num_tokens
 
-    def _replicate_from(self, other, row_begin, n_rows, n_tokens):
-        """HIP copy of row 0, positions [0, n_tokens), of every slot of `other` into rows
+    def _replicate_from(self, other, row_begin, n_rows, n_tokens, src_row=0):
+        """HIP copy of row `src_row`, positions [0, n_tokens), of every slot of `other` into rows
         [row_begin, row_begin + n_rows) of this cache."""
         _ext.require_rocm(self.k_cache, other.k_cache, what="KVCache replication")
         if self.k_cache.dtype != other.k_cache.dtype:
@@ -80,8 +80,11 @@ class KVCache:
             return
         row_elems = self.n_kv_head * self.head_dim
         lib = _ext.lib()
+        assert 0 <= src_row < other.batch_size, f"source row {src_row} out of range"
+        src_off = src_row * other.k_cache.stride(1) * other.k_cache.element_size()
         st = lib.mcamd_kv_replicate(
-            other.k_cache.data_ptr(), other.v_cache.data_ptr(), self.k_cache.data_ptr(),
+            other.k_cache.data_ptr() + src_off, other.v_cache.data_ptr() + src_off,
+            self.k_cache.data_ptr(),
             self.v_cache.data_ptr(), self.n_slots, other.k_cache.stride(0),
             self.k_cache.stride(0), self.batch_size, self.k_cache.stride(1), row_begin, n_rows,
             n_tokens, row_elems,
@@ -106,6 +109,28 @@ class KVCache:
         # Expand any batch=1 extra state to every row.
         for key, value in other.state.items():
             self.state[key] = value.expand(self.batch_size, *([-1] * (value.dim() - 1))).clone()
+
+    def prefill_rows(self, other, lengths, num_samples=1):
+        """Copy the prompts of a cache prefilled together -- row p of `other` holds prompt p,
+        right-padded to the longest -- into rows [p * num_samples, (p + 1) * num_samples), each
+        ending at its prompt's length (right-ragged). The batched counterpart of calling
+        prefill_row once per prompt and sample (modelcore/cache.py:92-119), without its host
+        reads: the lengths are given. Positions past a row's length hold the padding's K/V, which
+        attention never reads (they lie beyond cache_seqlens) and decode overwrites."""
+        lengths = [int(n) for n in lengths]
+        assert other.batch_size == len(lengths), "one source row per prompt length"
+        assert self.batch_size == len(lengths) * num_samples, \
+            f"batch_size {self.batch_size} != {len(lengths)} prompts x {num_samples} samples"
+        assert self.get_pos() == 0, "Cannot prefill a non-empty KV cache"
+        self._assert_same_geometry(other)
+        assert not other.state, "per-row extra state is not carried by the batched prefill"
+        for p, n in enumerate(lengths):
+            assert 0 < n <= other.max_seq_len, f"prompt length {n} out of range"
+            assert n <= self.max_seq_len, f"prompt of {n} tokens exceeds cache length {self.max_seq_len}"
+            self._replicate_from(other, p * num_samples, num_samples, n, src_row=p)
+        per_row = [n for n in lengths for _ in range(num_samples)]
+        self.cache_seqlens.copy_(torch.tensor(per_row, dtype=torch.int32))
+        self._pos_uniform = per_row[0] if len(set(per_row)) == 1 else None
 
     def prefill_row(self, row, other):
         """Copy a batch=1 prefilled cache into row `row` only (modelcore/cache.py:92-119); rows

@@ -15,9 +15,8 @@
 // banks) and are summed in a fixed order -- the result does not depend on timing -- then written
 // as bf16 with consecutive lanes on consecutive n. Rows m >= M of x read as zero.
 //
-// Loads are issued one group of four k-steps ahead of the products that use them, from the
-// registers of a second buffer, so each wave keeps ~8-16 KiB of W in flight; one workgroup
-// (eight waves) per CU keeps the HBM queue full.
+// Loads are issued one group of U (4 or 8) k-steps ahead of the products that use them, into the
+// registers of a second buffer, so each wave keeps 4-8 KiB of W in flight.
 #include "kernels.h"
 
 namespace mcamd {
@@ -25,10 +24,6 @@ namespace {
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-#ifndef MCAMD_LIN_U
-#define MCAMD_LIN_U 4
-#endif
-constexpr int U = MCAMD_LIN_U;  // k-steps per load group
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -55,7 +50,7 @@ __device__ __forceinline__ uint16_t to_bf16(float x) {
   return uint16_t(u >> 16);
 }
 
-template <int RB, int MB>
+template <int RB, int MB, int U>
 __global__ __launch_bounds__(kThreads, 1) void linear_skinny_kernel(LinParams P) {
   constexpr int NR = RB * 32;      // rows of W (outputs n) per workgroup
   constexpr int MP = MB * 32 + 1;  // padded m stride of the LDS partials
@@ -156,8 +151,17 @@ __global__ __launch_bounds__(kThreads, 1) void linear_skinny_kernel(LinParams P)
 
 template <int RB, int MB>
 void launch(const LinParams &P, hipStream_t stream) {
-  hipLaunchKernelGGL((linear_skinny_kernel<RB, MB>), dim3(unsigned(P.N / (RB * 32))),
-                     dim3(kThreads), 0, stream, P);
+  // Eight k-steps per load group where the K-slices allow it (twice the bytes in flight), else
+  // four; 64-row groups with two x blocks keep four (eight would spill).
+  const dim3 grid(unsigned(P.N / (RB * 32)));
+  if constexpr (RB == 2 && MB == 2) {
+    hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 4>), grid, dim3(kThreads), 0, stream, P);
+  } else {
+    if (P.K % (16 * 8 * kWaves) == 0)
+      hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 8>), grid, dim3(kThreads), 0, stream, P);
+    else
+      hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 4>), grid, dim3(kThreads), 0, stream, P);
+  }
 }
 
 }  // namespace
@@ -170,7 +174,7 @@ extern "C" int mcamd_linear_bf16(const void *x, int64_t ldx, const void *w, void
                                  void *stream) {
   if (m < 0 || m > 64)
     return fail(MCAMD_EUNSUPPORTED, "linear_bf16: m must be at most 64 (decode-sized batches)");
-  if (n <= 0 || k <= 0 || n % 32 != 0 || k % (16 * U * kWaves) != 0)
+  if (n <= 0 || k <= 0 || n % 32 != 0 || k % (16 * 4 * kWaves) != 0)
     return fail(MCAMD_EUNSUPPORTED, "linear_bf16: n must be a multiple of 32 and k of 512");
   if (n > (int64_t(1) << 30) || k > (int64_t(1) << 30))
     return fail(MCAMD_EUNSUPPORTED, "linear_bf16: n or k too large");

@@ -3,8 +3,9 @@
 
 ``Decoder`` prefills a prompt at batch 1, replicates its cache into ``num_samples`` rows with the
 HIP replication kernel (``KVCache.prefill``), then steps every row one position per call. Several
-prompts are prefilled one at a time and copied into their own right-ragged rows
-(``KVCache.prefill_row``); row ``p * num_samples + s`` is sample ``s`` of prompt ``p``.
+prompts are prefilled together, right-padded to the longest, and each is copied into its own
+right-ragged rows (``KVCache.prefill_rows``); row ``p * num_samples + s`` is sample ``s`` of
+prompt ``p``.
 """
 from __future__ import annotations
 
@@ -38,28 +39,35 @@ class Decoder:
         if isinstance(tokens[0], int):
             prefill = manager.new_kv_cache(model, batch_size=1, seq_len=len(tokens), device=device)
             ids = torch.tensor([tokens], dtype=torch.long, device=device)
-            logits = model.forward(ids, kv_cache=prefill)
-            self._logits = logits[:, -1, :].expand(num_samples, -1)
+            logits = model.last_logits(ids, prefill, torch.tensor([len(tokens) - 1]))
+            self._logits = logits.expand(num_samples, -1)
             length = len(tokens) + max_tokens if max_tokens is not None \
                 else model.config.sequence_len
             self.kv_cache = manager.new_kv_cache(model, batch_size=num_samples, seq_len=length,
                                                  device=device)
             self.kv_cache.prefill(prefill)
             return
+        # Several prompts: one batched prefill of the prompts right-padded to the longest (causal
+        # attention keeps every prompt's positions blind to its padding), then each prompt's row
+        # copied into its samples' rows at its own length -- in place of the reference's prefill
+        # and prefill_row per prompt (modelcore/generate.py:67-80), with no host reads.
         prompts = [list(p) for p in tokens]
-        length = max(map(len, prompts)) + max_tokens if max_tokens is not None \
-            else model.config.sequence_len
+        lengths = [len(p) for p in prompts]
+        assert min(lengths) > 0, "empty prompt"
+        longest = max(lengths)
+        length = longest + max_tokens if max_tokens is not None else model.config.sequence_len
+        prefill = manager.new_kv_cache(model, batch_size=len(prompts), seq_len=longest,
+                                       device=device)
+        ids = torch.zeros(len(prompts), longest, dtype=torch.long)
+        for p, prompt in enumerate(prompts):
+            ids[p, :len(prompt)] = torch.tensor(prompt, dtype=torch.long)
+        last = torch.tensor(lengths) - 1
+        logits = model.last_logits(ids.to(device), prefill, last)
         self.kv_cache = manager.new_kv_cache(model, batch_size=len(prompts) * num_samples,
                                              seq_len=length, device=device)
-        rows = []
-        for p, prompt in enumerate(prompts):
-            prefill = manager.new_kv_cache(model, batch_size=1, seq_len=len(prompt), device=device)
-            ids = torch.tensor([prompt], dtype=torch.long, device=device)
-            rows.append(model.forward(ids, kv_cache=prefill)[:, -1, :].expand(num_samples, -1))
-            for s in range(num_samples):
-                self.kv_cache.prefill_row(p * num_samples + s, prefill)
-            del prefill
-        self._logits = torch.cat(rows, dim=0)
+        self.kv_cache.prefill_rows(prefill, lengths, num_samples)
+        del prefill
+        self._logits = logits.repeat_interleave(num_samples, dim=0)
 
     @property
     def logits(self):

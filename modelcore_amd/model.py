@@ -626,6 +626,15 @@ class Model(nn.Module):
             kv_cache.advance(idx.size(1))
         return self.unembedding(x)
 
+    def last_logits(self, idx, kv_cache, last):
+        """forward(), but the head runs only at position last[b] of row b: (B, vocab) logits.
+        The head is per position, so these equal forward()[b, last[b]]; a prompt prefill needs
+        only its last position, and skips the (B, T, vocab) logits of all the others."""
+        x = self.body(self.embedding(idx), kv_cache)
+        kv_cache.advance(idx.size(1))
+        rows = torch.arange(idx.size(0), device=x.device)
+        return self.unembedding(x[rows, last.to(x.device)].unsqueeze(1))[:, 0]
+
 
 def kv_cache_spec(layer_specs):
     """num_kv_slots / n_kv_head / head_dim for KVCache (modelcore/stats.py:110-131): one slot per

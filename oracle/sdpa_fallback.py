@@ -94,10 +94,10 @@ def replicate(dst_k, dst_v, src_k, src_v, n_tokens):
     dst_v[:, :, :n_tokens] = src_v[:, :, :n_tokens]
 
 
-def replicate_rows(dst, src, row_begin, n_rows, n_tokens):
-    """KVCache-level copy of row 0, positions [0, n_tokens), of every slot of `src` into rows
-    [row_begin, row_begin + n_rows) of `dst` (modelcore/cache.py:84-85 and :106-107); the same
-    argument meaning as modelcore_amd.cache.KVCache._replicate_from, for CPU caches."""
+def replicate_rows(dst, src, row_begin, n_rows, n_tokens, src_row=0):
+    """KVCache-level copy of row `src_row`, positions [0, n_tokens), of every slot of `src` into
+    rows [row_begin, row_begin + n_rows) of `dst` (modelcore/cache.py:84-85 and :106-107); the
+    same argument meaning as modelcore_amd.cache.KVCache._replicate_from, for CPU caches."""
     rows = slice(row_begin, row_begin + n_rows)
-    dst.k_cache[:, rows, :n_tokens] = src.k_cache[:, 0:1, :n_tokens]
-    dst.v_cache[:, rows, :n_tokens] = src.v_cache[:, 0:1, :n_tokens]
+    dst.k_cache[:, rows, :n_tokens] = src.k_cache[:, src_row:src_row + 1, :n_tokens]
+    dst.v_cache[:, rows, :n_tokens] = src.v_cache[:, src_row:src_row + 1, :n_tokens]

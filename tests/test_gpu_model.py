@@ -44,10 +44,10 @@ def cpu_cache_copies(monkeypatch):
     from modelcore_amd.cache import KVCache
     real = KVCache._replicate_from
 
-    def copy(self, other, r0, n, t):
+    def copy(self, other, r0, n, t, src_row=0):
         if self.k_cache.device.type == "cpu":
-            return sdpa_fallback.replicate_rows(self, other, r0, n, t)
-        return real(self, other, r0, n, t)
+            return sdpa_fallback.replicate_rows(self, other, r0, n, t, src_row)
+        return real(self, other, r0, n, t, src_row)
 
     monkeypatch.setattr(KVCache, "_replicate_from", copy)
 
@@ -283,3 +283,38 @@ def test_captured_decode_step_replays_the_eager_steps():
     torch.cuda.synchronize()
     assert dec.kv_cache.cache_seqlens.tolist() == [90 + n] * R
     assert torch.equal(dec.kv_cache.k_cache[:, :, :90 + n], eager.kv_cache.k_cache[:, :, :90 + n])
+
+
+def test_batched_multi_prompt_prefill_matches_one_prefill_per_prompt():
+    """Ragged prompts prefilled together (right-padded, then KVCache.prefill_rows) against the
+    reference's flow of one prefill and prefill_row per prompt, bf16 on the GPU: the same
+    lengths, caches and logits within bf16 rounding, also after decode steps fed the same
+    tokens."""
+    _note("batched multi-prompt prefill")
+    cfg = mixed_window_config(n_layer=4)
+    mgr = gpu_manager(torch.bfloat16)
+    model = awake(mgr.create_model(cfg, device=DEV, seed=0))
+    g = torch.Generator().manual_seed(6)
+    lengths, S, steps = [37, 150, 5, 88], 2, 4
+    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in lengths]
+    dec = mgr.new_decoder(model, prompts, num_samples=S, max_tokens=steps + 1)
+    ref = mgr.new_kv_cache(model, batch_size=len(prompts) * S, seq_len=150 + steps + 1)
+    ref_logits = []
+    with torch.no_grad():
+        for p, prompt in enumerate(prompts):
+            one = mgr.new_kv_cache(model, batch_size=1, seq_len=len(prompt))
+            ref_logits.append(model(torch.tensor([prompt], device=DEV), kv_cache=one)[:, -1])
+            for s in range(S):
+                ref.prefill_row(p * S + s, one)
+    assert dec.kv_cache.cache_seqlens.tolist() == ref.cache_seqlens.tolist()
+    for r, n in enumerate(ref.cache_seqlens.tolist()):
+        for a, b in ((dec.kv_cache.k_cache, ref.k_cache), (dec.kv_cache.v_cache, ref.v_cache)):
+            assert (a[:, r, :n].float() - b[:, r, :n].float()).abs().max() <= 0.1, r
+    want = torch.cat(ref_logits).repeat_interleave(S, 0).float()
+    assert (dec.logits.float() - want).abs().max() <= 0.1
+    feed = torch.randint(0, cfg.vocab_size, (steps, len(prompts) * S), generator=g).to(DEV)
+    with torch.no_grad():
+        for t in range(steps):
+            a = dec.step(feed[t]).float()
+            b = model(feed[t].view(-1, 1), kv_cache=ref)[:, -1].float()
+            assert (a - b).abs().max() <= 0.1, t

@@ -31,7 +31,8 @@ def cpu_cache_copies(monkeypatch):
     copy stands in for it, so Decoder can be exercised here."""
     from modelcore_amd.cache import KVCache
     monkeypatch.setattr(KVCache, "_replicate_from",
-                        lambda self, other, r0, n, t: sdpa_fallback.replicate_rows(self, other, r0, n, t))
+                        lambda self, other, r0, n, t, src_row=0:
+                        sdpa_fallback.replicate_rows(self, other, r0, n, t, src_row))
 
 
 def manager():
@@ -195,3 +196,47 @@ def test_the_default_operator_refuses_cpu_tensors():
     model = mgr.create_model(tiny_config(), device=CPU, seed=0)
     with pytest.raises(RuntimeError, match="ROCm device"):
         model(torch.tensor([[1, 2, 3]]))
+
+
+def test_batched_prompt_prefill_equals_one_prefill_per_prompt():
+    """The Decoder's batched prefill (prompts right-padded to the longest, then prefill_rows)
+    leaves the caches and first logits the reference's per-prompt prefill + prefill_row leave
+    (modelcore/generate.py:67-80), within fp32 rounding; rows end at their own lengths."""
+    mgr = manager()
+    model = awake(mgr.create_model(tiny_config(kv_share=True), device=CPU, seed=0))
+    prompts = [[4, 8, 15], [16, 23, 42, 4, 8, 15, 16], [1]]
+    S, extra = 2, 5
+    dec = mgr.new_decoder(model, prompts, num_samples=S, max_tokens=extra)
+    assert dec.kv_cache.cache_seqlens.tolist() == [3, 3, 7, 7, 1, 1]
+    assert dec.kv_cache.uniform_pos() is None
+    ref = mgr.new_kv_cache(model, batch_size=len(prompts) * S, seq_len=7 + extra)
+    ref_logits = []
+    for p, prompt in enumerate(prompts):
+        one = mgr.new_kv_cache(model, batch_size=1, seq_len=len(prompt))
+        with torch.no_grad():
+            ref_logits.append(model(torch.tensor([prompt]), kv_cache=one)[:, -1])
+        for s in range(S):
+            ref.prefill_row(p * S + s, one)
+    assert ref.cache_seqlens.tolist() == dec.kv_cache.cache_seqlens.tolist()
+    for r in range(len(prompts) * S):
+        n = int(ref.cache_seqlens[r])
+        torch.testing.assert_close(dec.kv_cache.k_cache[:, r, :n], ref.k_cache[:, r, :n],
+                                   rtol=1e-5, atol=1e-6)
+        torch.testing.assert_close(dec.kv_cache.v_cache[:, r, :n], ref.v_cache[:, r, :n],
+                                   rtol=1e-5, atol=1e-6)
+    want = torch.cat(ref_logits).repeat_interleave(S, 0)
+    torch.testing.assert_close(dec.logits, want, rtol=1e-5, atol=1e-6)
+
+
+def test_prefill_rows_refuses_what_it_cannot_place():
+    mgr = manager()
+    model = mgr.create_model(tiny_config(), device=CPU, seed=0)
+    src = mgr.new_kv_cache(model, batch_size=2, seq_len=6)
+    with pytest.raises(AssertionError, match="prompts x"):
+        mgr.new_kv_cache(model, batch_size=3, seq_len=8).prefill_rows(src, [3, 6], 2)
+    with pytest.raises(AssertionError, match="exceeds cache length"):
+        mgr.new_kv_cache(model, batch_size=2, seq_len=4).prefill_rows(src, [3, 6], 1)
+    dst = mgr.new_kv_cache(model, batch_size=2, seq_len=8)
+    dst.advance(1)
+    with pytest.raises(AssertionError, match="non-empty"):
+        dst.prefill_rows(src, [3, 6], 1)
