@@ -167,13 +167,16 @@ int mcamd_qk_rope_norm_append(const void *q, int64_t q_token_stride, const void 
 /*
  * y = x . W^T for decode-sized batches: x (m, k) bf16 rows `ldx` elements apart, m <= 64; W
  * (n, k) bf16 contiguous (the nn.Linear weight layout); y (m, n) bf16 rows `ldy` apart; fp32
- * accumulation in a fixed order (deterministic). n must be a multiple of 32 and k of 512;
- * rows_per_group (32 or 64) is the number of W rows one workgroup streams.
+ * accumulation. n must be a multiple of 64 and k of 128 * k_splits. With k_splits > 1 the K
+ * range is split across workgroups and the partial products are summed in a fixed order by a
+ * second kernel (deterministic), using `workspace` of mcamd_linear_bf16_workspace_bytes() bytes.
  * Replaces F.linear in Linear.forward (modelcore/components/linear.py:13-14) for the projections
  * of a decode step, where reading the weights once from HBM is the whole cost.
  */
+size_t mcamd_linear_bf16_workspace_bytes(int64_t m, int64_t n, int64_t k_splits);
 int mcamd_linear_bf16(const void *x, int64_t ldx, const void *w, void *y, int64_t ldy, int64_t m,
-                      int64_t n, int64_t k, int rows_per_group, void *stream);
+                      int64_t n, int64_t k, int64_t k_splits, void *workspace,
+                      size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -2,46 +2,47 @@
 // nn.Linear weight layout), y (M, N) bf16, fp32 accumulation.
 //
 // Replaces F.linear in Linear.forward (modelcore/components/linear.py:13-14) when a decode step
-// feeds at most 64 rows: there every weight byte is used M times, so the product is bound by
-// reading W from HBM once, and a library GEMM tiled for large M leaves much of that bandwidth
-// unused on these shapes.
+// feeds at most 64 rows: every weight byte is then used at most 64 times, so the product is bound
+// by reading W from HBM once.
 //
-// Work split. A workgroup of eight waves owns RB * 32 consecutive rows of W (outputs n) and the
-// whole K; wave w takes the K-slice [w K / 8, (w + 1) K / 8). Per 16-wide k-step a wave loads RB
-// fragments of W (32 rows x 16 k, 16 bytes per lane) and MB fragments of x (32 rows x 16 k) and
-// runs RB * MB v_mfma_f32_32x32x16_bf16 with W as the A operand and x as the B operand, so the
-// accumulators hold y^T blocks: n = 8 (r / 4) + 4 h + r % 4 of the block, m = lane % 32. The
-// eight K-slice partials meet in LDS (padded so neither the writes nor the reads collide in
-// banks) and are summed in a fixed order -- the result does not depend on timing -- then written
-// as bf16 with consecutive lanes on consecutive n. Rows m >= M of x read as zero.
+// Work split. A workgroup of four waves owns 64 consecutive rows of W (outputs n) and a K-range
+// [k0, k0 + K / S): S = 1 when there are enough 64-row tiles to fill the GPU, else the K-range is
+// split S ways and the S partial products are summed by a second pass in a fixed order (results
+// never depend on timing). Wave w owns rows 16 w .. 16 w + 15 of the tile; all four share the
+// activation rows.
 //
-// Loads are issued one group of U (4 or 8) k-steps ahead of the products that use them, into the
-// registers of a second buffer, so each wave keeps 4-8 KiB of W in flight.
+// Data path. The K-range is walked in stages of 128: one stage is 64 rows x 256 bytes of W and
+// 64 rows x 256 bytes of x, brought into LDS by buffer_load ... lds (16 bytes per lane, four rows
+// of 256 contiguous bytes per instruction, so every HBM line is read whole), three stages ahead,
+// in a ring of four. The buffer resources bound every read (rows of x past M read as zero). In
+// LDS a row keeps its sixteen 16-byte chunks, chunk c of row r at slot c ^ (r % 16), so the
+// fragment reads below -- sixteen rows, one chunk each -- fall on distinct banks.
+//
+// Products: v_mfma_f32_16x16x32_bf16 with A = 16 rows of W x 32 k (lane l: row l % 16, k 8 (l / 16)
+// .. + 7), B = 32 k x 16 rows of x, four blocks for M = 64; accumulators D[n][m] with lane l
+// holding n = 4 (l / 16) + i, m = l % 16.
 #include "kernels.h"
 
 namespace mcamd {
 namespace {
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
+constexpr int kRows = 16 * kWaves;  // rows of W per workgroup
+constexpr int KC = 128;             // k per stage
+constexpr int kRing = 4;            // LDS stages
+constexpr int kStage = 64 * KC;     // elements of one W (or x) stage
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct LinParams {
   const uint16_t *x, *w;
   uint16_t *y;
+  float *part;  // [S][M][N] fp32 partials when S > 1
   int64_t ldx, ldy;
-  int M, N, K;
+  int M, N, K, S;
 };
-
-__device__ __forceinline__ f32x16 mfma(const bf16x8 &a, const bf16x8 &b, const f32x16 &c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ bf16x8 load16(const uint16_t *p) {
-  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(p));
-}
 
 __device__ __forceinline__ uint16_t to_bf16(float x) {
   uint32_t u = __float_as_uint(x);
@@ -50,118 +51,115 @@ __device__ __forceinline__ uint16_t to_bf16(float x) {
   return uint16_t(u >> 16);
 }
 
-template <int RB, int MB, int U>
+template <int MB>  // blocks of 16 activation rows: M <= 16 MB
 __global__ __launch_bounds__(kThreads, 1) void linear_skinny_kernel(LinParams P) {
-  constexpr int NR = RB * 32;      // rows of W (outputs n) per workgroup
-  constexpr int MP = MB * 32 + 1;  // padded m stride of the LDS partials
-  __shared__ float part[kWaves * NR * MP];  // [wave][n][m]
+  __shared__ __attribute__((aligned(1024))) uint16_t sW[kRing][kStage];
+  __shared__ __attribute__((aligned(1024))) uint16_t sX[kRing][kStage];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int h = lane >> 5;
-  const int col = lane & 31;
-  const int n0 = blockIdx.x * NR;
-  const int ks = P.K / kWaves;  // this wave's K-slice, a multiple of 16 * U
-  const int k_begin = wave * ks;
-  const int steps = ks / 16;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * kRows;
+  const int ks = P.K / P.S;
+  const int k_begin = blockIdx.y * ks;
+  const int stages = ks / KC;
 
-  const uint16_t *wrow[RB];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
-    wrow[rb] = P.w + int64_t(n0 + rb * 32 + col) * P.K + k_begin + 8 * h;
-  const uint16_t *xrow[MB];
-  bool xlive[MB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int m = mb * 32 + col;
-    xlive[mb] = m < P.M;
-    xrow[mb] = P.x + int64_t(xlive[mb] ? m : 0) * P.ldx + k_begin + 8 * h;
-  }
+  const uint32_t wbytes = uint32_t(kRows) * uint32_t(P.K) * 2u;
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(P.w + int64_t(n0) * P.K), 0, int(wbytes), 0x00020000);
+  const uint32_t xbytes = uint32_t(P.M) * uint32_t(P.ldx) * 2u;
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void *)P.x, 0, int(xbytes), 0x00020000);
 
-  f32x16 acc[RB][MB];
+  // DMA: instruction j (0..15) of a stage moves rows 4 j .. 4 j + 3; wave w issues j = 4 w .. 4 w
+  // + 3 for W and for x. Lane i lands at LDS slot i % 16 of row 4 j + i / 16 and reads the
+  // global chunk that belongs there.
+  const int drow = lane >> 4;
+  const int dslot = lane & 15;
+  auto issue_stage = [&](int st, int buf) {
+    const uint32_t kb = uint32_t(k_begin + st * KC) * 2u;
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[rb][mb][e] = 0.f;
-
-  const bf16x8 zero8 = {};
-  bf16x8 wa[2][U][RB], xb[2][U][MB];
-  auto load_group = [&](int buf, int s0) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int off = 16 * (s0 + u);
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) wa[buf][u][rb] = load16(wrow[rb] + off);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        // Unconditional load (dead rows read row 0), then a select: no branch between the
-        // loads, so the waits before the products count them exactly.
-        const bf16x8 v = load16(xrow[mb] + off);
-        xb[buf][u][mb] = xlive[mb] ? v : zero8;
-      }
+    for (int jj = 0; jj < 4; ++jj) {
+      const int r = 4 * (4 * wave + jj) + drow;
+      const uint32_t chunk = uint32_t(dslot ^ (r & 15));
+      const uint32_t wo = uint32_t(r) * uint32_t(P.K) * 2u + kb + chunk * 16u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rw, (__attribute__((address_space(3))) void *)(&sW[buf][(4 * (4 * wave + jj)) * KC]),
+          16, int(wo), 0, 0, 0);
+      const uint32_t xo = uint32_t(r) * uint32_t(P.ldx) * 2u + kb + chunk * 16u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rx, (__attribute__((address_space(3))) void *)(&sX[buf][(4 * (4 * wave + jj)) * KC]),
+          16, int(xo), 0, 0, 0);
     }
   };
-  auto mul_group = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-          acc[rb][mb] = mfma(wa[buf][u][rb], xb[buf][u][mb], acc[rb][mb]);
-  };
 
-  load_group(0, 0);
-  int g = 0;
-  for (; g + U < steps; g += 2 * U) {
-    load_group(1, g + U);
-    mul_group(0);
-    // Unconditional (the last pass reloads a group it already has), so the waits before the
-    // products count the loads exactly.
-    load_group(0, min(g + 2 * U, steps - U));
-    mul_group(1);
-  }
-  if (g < steps) mul_group(0);
+  f32x4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Partials into LDS: part[wave][n][m], m contiguous (lanes of a half write consecutive m).
-  float *mine = part + wave * NR * MP;
+  const int fr = lane & 15;  // fragment row (W row within the wave's 16, or x row in a block)
+  const int fq = lane >> 4;  // which 8 k of the 32
+  const int wr = 16 * wave + fr;
+
+  // Stages 0..2 before the loop; stage st + 3 goes into buffer (st + 3) % 4, last read in
+  // iteration st - 1, after the barrier of iteration st. Each stage is 8 loads per wave.
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+  for (int st = 0; st < kRing - 1; ++st)
+    if (st < stages) issue_stage(st, st);
+  for (int st = 0; st < stages; ++st) {
+    const int ahead = min(stages - 1 - st, kRing - 2);  // younger stages that may stay pending
+    if (ahead >= 2)
+      __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16)
+    else if (ahead == 1)
+      __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    if (st + kRing - 1 < stages) issue_stage(st + kRing - 1, (st + kRing - 1) % kRing);
+    const uint16_t *tw = sW[st % kRing];
+    const uint16_t *tx = sX[st % kRing];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+    for (int s = 0; s < KC / 32; ++s) {
+      const int c = 4 * s + fq;
+      const bf16x8 a = __builtin_bit_cast(
+          bf16x8, *reinterpret_cast<const uint4 *>(&tw[wr * KC + ((c ^ (wr & 15)) << 3)]));
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int n = rb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        mine[n * MP + mb * 32 + col] = acc[rb][mb][r];
+      for (int mb = 0; mb < MB; ++mb) {
+        const int xr = 16 * mb + fr;
+        const bf16x8 b = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const uint4 *>(&tx[xr * KC + ((c ^ (xr & 15)) << 3)]));
+        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[mb], 0, 0, 0);
       }
-  __syncthreads();
-  // Sum the eight K-slices in wave order; consecutive threads take consecutive n.
-  for (int i = threadIdx.x; i < NR * MB * 32; i += kThreads) {
-    const int n = i % NR;
-    const int m = i / NR;
-    if (m >= P.M) break;
-    float s = 0.f;
+    }
+  }
+
+  // acc[mb][i] = y[m = 16 mb + l % 16][n = n0 + 16 w + 4 (l / 16) + i].
+  const int n = n0 + 16 * wave + 4 * fq;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) s += part[(w * NR + n) * MP + m];
-    P.y[int64_t(m) * P.ldy + n0 + n] = to_bf16(s);
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = 16 * mb + fr;
+    if (m >= P.M) continue;
+    if (P.S == 1) {
+      const uint32_t lo = uint32_t(to_bf16(acc[mb][0])) | (uint32_t(to_bf16(acc[mb][1])) << 16);
+      const uint32_t hi = uint32_t(to_bf16(acc[mb][2])) | (uint32_t(to_bf16(acc[mb][3])) << 16);
+      *reinterpret_cast<uint2 *>(P.y + int64_t(m) * P.ldy + n) = uint2{lo, hi};
+    } else {
+      *reinterpret_cast<f32x4 *>(P.part + (int64_t(blockIdx.y) * P.M + m) * P.N + n) = acc[mb];
+    }
   }
 }
 
-template <int RB, int MB>
-void launch(const LinParams &P, hipStream_t stream) {
-  // Eight k-steps per load group where the K-slices allow it (twice the bytes in flight), else
-  // four; 64-row groups with two x blocks keep four (eight would spill).
-  const dim3 grid(unsigned(P.N / (RB * 32)));
-  if constexpr (RB == 2 && MB == 2) {
-    hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 4>), grid, dim3(kThreads), 0, stream, P);
-  } else {
-    if (P.K % (16 * 8 * kWaves) == 0)
-      hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 8>), grid, dim3(kThreads), 0, stream, P);
-    else
-      hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 4>), grid, dim3(kThreads), 0, stream, P);
-  }
+// y[m][n] = sum over the S partials in order, four n per thread.
+__global__ __launch_bounds__(256) void linear_reduce_kernel(LinParams P) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;  // float4 index
+  const int64_t per_row = P.N / 4;
+  if (i >= int64_t(P.M) * per_row) return;
+  const int64_t m = i / per_row, n = (i - m * per_row) * 4;
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < P.S; ++k)
+    s += *reinterpret_cast<const f32x4 *>(P.part + (int64_t(k) * P.M + m) * P.N + n);
+  const uint32_t lo = uint32_t(to_bf16(s[0])) | (uint32_t(to_bf16(s[1])) << 16);
+  const uint32_t hi = uint32_t(to_bf16(s[2])) | (uint32_t(to_bf16(s[3])) << 16);
+  *reinterpret_cast<uint2 *>(P.y + m * P.ldy + n) = uint2{lo, hi};
 }
 
 }  // namespace
@@ -169,47 +167,62 @@ void launch(const LinParams &P, hipStream_t stream) {
 
 using namespace mcamd;
 
+extern "C" size_t mcamd_linear_bf16_workspace_bytes(int64_t m, int64_t n, int64_t k_splits) {
+  return k_splits > 1 ? size_t(k_splits) * size_t(m) * size_t(n) * sizeof(float) : 0;
+}
+
 extern "C" int mcamd_linear_bf16(const void *x, int64_t ldx, const void *w, void *y, int64_t ldy,
-                                 int64_t m, int64_t n, int64_t k, int rows_per_group,
-                                 void *stream) {
+                                 int64_t m, int64_t n, int64_t k, int64_t k_splits,
+                                 void *workspace, size_t workspace_bytes, void *stream) {
   if (m < 0 || m > 64)
     return fail(MCAMD_EUNSUPPORTED, "linear_bf16: m must be at most 64 (decode-sized batches)");
-  if (n <= 0 || k <= 0 || n % 32 != 0 || k % (16 * 4 * kWaves) != 0)
-    return fail(MCAMD_EUNSUPPORTED, "linear_bf16: n must be a multiple of 32 and k of 512");
-  if (n > (int64_t(1) << 30) || k > (int64_t(1) << 30))
+  if (k_splits < 1 || k_splits > 64)
+    return fail(MCAMD_EINVAL, "linear_bf16: k_splits must be in [1, 64]");
+  if (n <= 0 || k <= 0 || n % kRows != 0 || k % (KC * k_splits) != 0)
+    return fail(MCAMD_EUNSUPPORTED,
+                "linear_bf16: n must be a multiple of 64 and k of 128 * k_splits");
+  if (n > (int64_t(1) << 30) || int64_t(kRows) * k * 2 >= (int64_t(1) << 31))
     return fail(MCAMD_EUNSUPPORTED, "linear_bf16: n or k too large");
-  if (rows_per_group != 32 && rows_per_group != 64)
-    return fail(MCAMD_EINVAL, "linear_bf16: rows_per_group must be 32 or 64");
-  if (rows_per_group == 64 && n % 64 != 0)
-    return fail(MCAMD_EINVAL, "linear_bf16: rows_per_group 64 needs n a multiple of 64");
   if (m == 0) {
     clear_error();
     return MCAMD_OK;
   }
   if (!x || !w || !y) return fail(MCAMD_EINVAL, "linear_bf16: null pointer");
-  if (ldx < k || ldy < n) return fail(MCAMD_EINVAL, "linear_bf16: ldx < k or ldy < n");
-  if (!aligned(x, 16) || !aligned(w, 16) || ldx % 8 != 0)
-    return fail(MCAMD_EINVAL, "linear_bf16: x and w must be 16-byte aligned, ldx a multiple of 8");
+  if (ldx < k || ldy < n || ldy % 4 != 0 || ldx % 8 != 0)
+    return fail(MCAMD_EINVAL, "linear_bf16: need ldx >= k (a multiple of 8), ldy >= n (of 4)");
+  if (m * ldx * 2 >= (int64_t(1) << 31))
+    return fail(MCAMD_EUNSUPPORTED, "linear_bf16: activations too large");
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 8))
+    return fail(MCAMD_EINVAL, "linear_bf16: x and w must be 16-byte aligned, y 8-byte aligned");
+  if (k_splits > 1 &&
+      (!workspace || workspace_bytes < mcamd_linear_bf16_workspace_bytes(m, n, k_splits) ||
+       !aligned(workspace, 16)))
+    return fail(MCAMD_EWORKSPACE, "linear_bf16: workspace missing or too small for k_splits");
   LinParams P;
   P.x = static_cast<const uint16_t *>(x);
   P.w = static_cast<const uint16_t *>(w);
   P.y = static_cast<uint16_t *>(y);
+  P.part = static_cast<float *>(workspace);
   P.ldx = ldx;
   P.ldy = ldy;
   P.M = int(m);
   P.N = int(n);
   P.K = int(k);
+  P.S = int(k_splits);
   hipStream_t s = as_stream(stream);
-  if (rows_per_group == 64) {
-    if (m > 32)
-      launch<2, 2>(P, s);
-    else
-      launch<2, 1>(P, s);
-  } else {
-    if (m > 32)
-      launch<1, 2>(P, s);
-    else
-      launch<1, 1>(P, s);
-  }
-  return launch_status("linear_bf16");
+  const dim3 grid(unsigned(n / kRows), unsigned(k_splits));
+  if (m <= 16)
+    hipLaunchKernelGGL(linear_skinny_kernel<1>, grid, dim3(kThreads), 0, s, P);
+  else if (m <= 32)
+    hipLaunchKernelGGL(linear_skinny_kernel<2>, grid, dim3(kThreads), 0, s, P);
+  else if (m <= 48)
+    hipLaunchKernelGGL(linear_skinny_kernel<3>, grid, dim3(kThreads), 0, s, P);
+  else
+    hipLaunchKernelGGL(linear_skinny_kernel<4>, grid, dim3(kThreads), 0, s, P);
+  int st = launch_status("linear_bf16");
+  if (st != MCAMD_OK || k_splits == 1) return st;
+  const int64_t quads = m * (n / 4);
+  hipLaunchKernelGGL(linear_reduce_kernel, dim3(unsigned((quads + 255) / 256)), dim3(256), 0, s,
+                     P);
+  return launch_status("linear_bf16 reduce");
 }

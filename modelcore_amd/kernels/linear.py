@@ -3,9 +3,10 @@ activations, the projection GEMMs of a decode step (``F.linear`` in the referenc
 ``Linear.forward``, modelcore/components/linear.py:13-14).
 
 With 64 or fewer rows each weight byte is used at most 64 times, so the product is bound by
-reading W once from HBM; ``mcamd_linear_bf16`` streams W with a K-split inside each workgroup
-and sums the partials in a fixed order (deterministic, fp32 accumulation). ``supported`` says
-which shapes it takes; the caller keeps ``F.linear`` for the rest (prefill-sized batches, fp32).
+reading W once from HBM. ``mcamd_linear_bf16`` streams 64-row tiles of W (and the activations)
+through LDS with coalesced loads; when N has too few tiles to fill the GPU the K range is split
+and the partial products are summed in a fixed order by a second kernel (deterministic, fp32
+accumulation). ``supported`` says which shapes it takes.
 """
 from __future__ import annotations
 
@@ -13,9 +14,13 @@ import torch
 
 from modelcore_amd import _ext
 
-__all__ = ["supported", "linear_bf16"]
+__all__ = ["supported", "linear_bf16", "k_splits"]
 
 MAX_ROWS = 64
+TILE_N = 64     # rows of W per workgroup
+STAGE_K = 128   # k per pipeline stage
+_CUS = 256
+_WS: dict = {}
 
 
 def supported(x: torch.Tensor, w: torch.Tensor) -> bool:
@@ -24,32 +29,62 @@ def supported(x: torch.Tensor, w: torch.Tensor) -> bool:
             or w.device != x.device or w.dim() != 2 or not w.is_contiguous():
         return False
     n, k = w.shape
-    if x.shape[-1] != k or n % 32 or k % 512:
+    if x.shape[-1] != k or n % TILE_N or k % STAGE_K or TILE_N * k * 2 >= 2 ** 31:
         return False
     rows = x.numel() // k if k else 0
     return 0 < rows <= MAX_ROWS
 
 
-def _rows_per_group(n: int) -> int:
-    # 64 W rows per workgroup halves the activation re-reads but halves the workgroups; keep at
-    # least ~2 k workgroups' worth of waves for the wide projections only.
-    return 64 if n % 64 == 0 and n >= 16384 else 32
+def k_splits(m: int, n: int, k: int) -> int:
+    """The K split that minimises (weight bytes + partial traffic) / occupancy of one workgroup
+    per CU: 1 for wide projections, more when N has few 64-row tiles."""
+    tiles = n // TILE_N
+    best, best_cost = 1, None
+    for s in (1, 2, 4, 8, 16):
+        if k % (STAGE_K * s):
+            continue
+        groups = tiles * s
+        rounds = -(-groups // _CUS)
+        efficiency = groups / (rounds * _CUS)
+        partial = 2 * s * m * n * 4 if s > 1 else 0
+        cost = (n * k * 2 + partial) / efficiency
+        if best_cost is None or cost < best_cost * 0.98:
+            best, best_cost = s, cost
+    return best
 
 
-def linear_bf16(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+def _workspace(device, nbytes):
+    if nbytes == 0:
+        return None
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _WS.get(idx)
+    if ws is not None and ws.numel() >= nbytes:
+        return ws
+    if torch.cuda.is_current_stream_capturing():  # a buffer of the graph's own pool
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    ws = _WS[idx] = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+    return ws
+
+
+def linear_bf16(x: torch.Tensor, w: torch.Tensor, splits: int | None = None) -> torch.Tensor:
     """(..., k) bf16 x (n, k) bf16 -> (..., n) bf16, for at most 64 rows of x."""
     _ext.require_rocm(x, w, what="linear_bf16")
     if not supported(x, w):
         raise ValueError(f"linear_bf16 takes bf16 x with <= {MAX_ROWS} rows and a contiguous bf16 "
-                         f"(n, k) weight, n % 32 == 0, k % 512 == 0; got x {tuple(x.shape)} "
-                         f"{x.dtype}, w {tuple(w.shape)} {w.dtype}")
+                         f"(n, k) weight, n % {TILE_N} == 0, k % {STAGE_K} == 0; got x "
+                         f"{tuple(x.shape)} {x.dtype}, w {tuple(w.shape)} {w.dtype}")
     n, k = w.shape
     x2 = x.reshape(-1, k)
     if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
         x2 = x2.contiguous()
-    y = torch.empty(x2.shape[0], n, dtype=torch.bfloat16, device=x.device)
-    st = _ext.lib().mcamd_linear_bf16(x2.data_ptr(), x2.stride(0), w.data_ptr(), y.data_ptr(), n,
-                                      x2.shape[0], n, k, _rows_per_group(n),
-                                      _ext.stream_handle(x.device))
+    m = x2.shape[0]
+    s = splits if splits is not None else k_splits(m, n, k)
+    lib = _ext.lib()
+    need = lib.mcamd_linear_bf16_workspace_bytes(m, n, s)
+    ws = _workspace(x.device, need)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=x.device)
+    st = lib.mcamd_linear_bf16(x2.data_ptr(), x2.stride(0), w.data_ptr(), y.data_ptr(), n, m, n,
+                               k, s, ws.data_ptr() if ws is not None else None,
+                               ws.numel() if ws is not None else 0, _ext.stream_handle(x.device))
     _ext.check(st, "linear_bf16")
     return y.view(*x.shape[:-1], n)

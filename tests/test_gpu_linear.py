@@ -2,8 +2,8 @@
 same bf16 values (numpy), for the projection shapes of the decode workloads and edge sizes.
 
 Tolerance: the bf16 rounding of the output (2^-8 of |y|) plus fp32 accumulation, bounded by
-1e-5 of sum_k |x_k w_k|. The kernel sums its K-split partials in a fixed order, so two calls are
-bit-identical.
+1e-5 of sum_k |x_k w_k|. The kernel sums its K-split partials in a fixed order, so two calls with
+the same split are bit-identical.
 """
 import numpy as np
 import pytest
@@ -31,7 +31,8 @@ def _check(y, x, w):
 
 
 SHAPES = [(1, 1024, 512), (7, 4096, 4096), (33, 1024, 1536), (64, 14336, 4096),
-          (64, 4096, 14336), (32, 6144, 4096), (64, 32768, 1024)]
+          (64, 4096, 14336), (32, 6144, 4096), (64, 32768, 1024), (48, 28672, 4096),
+          (16, 4096, 4096)]
 
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
@@ -45,18 +46,15 @@ def test_products_match_float64(m, n, k):
     assert torch.equal(y, linear_bf16(x, w))  # deterministic
 
 
-@pytest.mark.parametrize("rpg", [32, 64])
-def test_both_workgroup_heights_give_the_same_bits(rpg, monkeypatch):
-    from modelcore_amd.kernels import linear as lin
-    _note("linear rows_per_group", rpg)
+@pytest.mark.parametrize("splits", [1, 2, 4, 8])
+def test_every_k_split_matches_float64(splits):
+    _note("linear k_splits", splits)
     g = torch.Generator().manual_seed(9)
     x = torch.randn(40, 2048, generator=g).to(torch.bfloat16).to(DEV)
     w = torch.randn(2048, 2048, generator=g).to(torch.bfloat16).to(DEV)
-    monkeypatch.setattr(lin, "_rows_per_group", lambda n: rpg)
-    y = linear_bf16(x, w)
+    y = linear_bf16(x, w, splits)
     _check(y, x, w)
-    monkeypatch.setattr(lin, "_rows_per_group", lambda n: 96 - rpg)
-    assert torch.equal(y, linear_bf16(x, w))  # same K split, same summation order
+    assert torch.equal(y, linear_bf16(x, w, splits))
 
 
 def test_strided_rows_and_leading_dims():
@@ -76,5 +74,6 @@ def test_unsupported_shapes_are_refused():
     assert not supported(x, w)
     with pytest.raises(ValueError):
         linear_bf16(x, w)
-    assert not supported(x[:8, :500], w[:, :500])  # k not a multiple of 512
+    assert not supported(x[:8, :500], w[:, :500])  # k not a multiple of 128
+    assert not supported(x[:8], w[:32])  # n not a multiple of 64
     assert not supported(x[:8].float(), w.float())
