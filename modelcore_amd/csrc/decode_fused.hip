@@ -62,6 +62,10 @@ constexpr int kMinKeysPerGroup = MCAMD_DECODE_MIN_KEYS;  // fewer workgroups whe
 #endif
 constexpr int kRing = MCAMD_DECODE_RING;  // tile buffers per wave (kRing - 1 tiles in flight)
 constexpr int kPart = KG * GM * D + 2 * KG * GM;  // floats per partial: o[16][D], (m, l)[16]
+#ifndef MCAMD_MERGE_BATCH
+#define MCAMD_MERGE_BATCH 8
+#endif
+constexpr int kMergeBatch = MCAMD_MERGE_BATCH;  // segments whose loads the merge keeps in flight
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -532,16 +536,16 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(FusedParams P) {
   if (nseg == 1) return;  // written directly by the streaming pass
   const float *base = P.part + int64_t(g_first + ug) * kPart;
   float M = -INFINITY, L = 0.f, t0 = 0.f, t1 = 0.f;
-  for (int s0 = 0; s0 < nseg; s0 += 8) {
-    float2 ml[8], v[8];
+  for (int s0 = 0; s0 < nseg; s0 += kMergeBatch) {
+    float2 ml[kMergeBatch], v[kMergeBatch];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < kMergeBatch; ++k) {
       const float *ps = base + int64_t(min(s0 + k, nseg - 1)) * kPart;
       ml[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * hr);
       v[k] = *reinterpret_cast<const float2 *>(ps + hr * D + 2 * lane);
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < kMergeBatch; ++k) {
       const float mk = s0 + k < nseg ? ml[k].x : -INFINITY;
       const float m_new = fmaxf(M, mk);
       const float fa = exp2_or_zero(M - m_new), fb = exp2_or_zero(mk - m_new);
