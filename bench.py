@@ -42,6 +42,8 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
+    ap.add_argument("--skinny-gemm", action="store_true",
+                    help="sample workload: run the decode projections through mcamd_linear_bf16")
     ap.add_argument("--workload", choices=("decode", "prefill", "replicate", "mixed", "sample"),
                     default="decode",
                     help="decode: the decode microbench (default, the headline metric); prefill: "
@@ -398,6 +400,7 @@ def bench_sample(args):
     log(f"building the {SM_LAYERS}-layer model on the GPU (seed 0)")
     model = mgr.create_model(cfg, device=dev, seed=0)
     model.cache_inference_weights()
+    model.use_skinny_gemm(args.skinny_gemm)
     prompt = torch.randint(0, SM_V, (SM_PROMPT,), generator=torch.Generator().manual_seed(0))
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -567,7 +570,9 @@ def main():
     # token fused into the split-K streaming pass (decode_fused_kernel), then the merge pass
     # (decode_merge_kernel) -- launched back to back through the C ABI on the stream they run on
     # and timed with HIP events around N launches. The positions stay put, so every launch
-    # rewrites the same new token and reads the same keys.
+    # rewrites the same new token and reads the same keys. Launches alternate between this cache
+    # and a second one of the same shape (as consecutive layers of a model would), so no launch
+    # finds the previous launch's keys in the 256 MB memory-side cache.
     lib = _ext.lib()
     pos = cache.cache_seqlens  # positions now: base + W + K, each row's query at its position
     out = torch.empty(B, 1, H, D, dtype=torch.bfloat16, device=dev)
@@ -575,20 +580,24 @@ def main():
     ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
     stream = _ext.stream_handle(dev)
     q1, k1, v1 = qd[0], kd[0], vd[0]
+    other = torch.randn(2, *k_slot.shape, device=dev,
+                        generator=torch.Generator(device=dev).manual_seed(1)).to(torch.bfloat16)
+    slots = [(k_slot, v_slot), (other[0], other[1])]
 
-    def decode_call():
+    def decode_call(i=0):
+        kc_i, vc_i = slots[i % 2]
         return lib.mcamd_flash_attn_with_kvcache(
-            q1.data_ptr(), k1.data_ptr(), v1.data_ptr(), k_slot.data_ptr(), v_slot.data_ptr(),
-            pos.data_ptr(), out.data_ptr(), B, 1, H, H_KV, D, t_alloc, k_slot.stride(0), -1, 1,
+            q1.data_ptr(), k1.data_ptr(), v1.data_ptr(), kc_i.data_ptr(), vc_i.data_ptr(),
+            pos.data_ptr(), out.data_ptr(), B, 1, H, H_KV, D, t_alloc, kc_i.stride(0), -1, 1,
             _ext.BF16, ws.data_ptr(), ws_bytes, stream)
 
-    for _ in range(5):
-        _ext.check(decode_call(), "flash_attn_with_kvcache")
+    for i in range(6):
+        _ext.check(decode_call(i), "flash_attn_with_kvcache")
     n_attn = max(K, 50)
     torch.cuda.synchronize()
     start.record()
-    for _ in range(n_attn):
-        decode_call()
+    for i in range(n_attn):
+        decode_call(i)
     end.record()
     torch.cuda.synchronize()
     attn_us = start.elapsed_time(end) / n_attn * 1e3

@@ -317,8 +317,8 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
         const bool is_new = fuse_new && t == pos;
         const uint16_t *kp = is_new ? P.k_new + new_off : kbase + int64_t(t) * tok_stride;
         const uint16_t *vp = is_new ? P.v_new + new_off : vbase + int64_t(t) * tok_stride;
-        Tl.k[j] = *reinterpret_cast<const uint4 *>(kp);
-        Tl.v[j] = *reinterpret_cast<const uint4 *>(vp);
+        Tl.k[j] = load_stream(kp);
+        Tl.v[j] = load_stream(vp);
       }
     };
 

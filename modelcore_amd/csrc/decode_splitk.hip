@@ -103,7 +103,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams P) 
       if (r < n) {
         const int t = t0 + r;
         const E *src = (t == pos && kn) ? kn + new_off : kc + row_base + int64_t(t) * tok_stride;
-        Vec<E>::load(src, kx[u]);
+        Vec<E>::unpack(load_stream(src), kx[u]);  // K/V are read once per pass
       } else {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) kx[u][e] = 0.f;
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams P) 
       if (r < n) {
         const int t = t0 + r;
         const E *src = (t == pos && vn) ? vn + new_off : vc + row_base + int64_t(t) * tok_stride;
-        Vec<E>::load(src, vx[u]);
+        Vec<E>::unpack(load_stream(src), vx[u]);  // K/V are read once per pass
       }
     }
 #pragma unroll

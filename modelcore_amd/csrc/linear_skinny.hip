@@ -44,6 +44,33 @@ struct LinParams {
   int M, N, K, S;
 };
 
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return uint32_t(uintptr_t((const __attribute__((address_space(3))) void *)(p)));
+}
+// LDS reads issued as inline asm: the compiler does not track them, so every use of a result sits
+// behind wait_lgkm, an explicit `s_waitcnt lgkmcnt(N)` that takes the results as operands.
+template <int OFF>
+__device__ __forceinline__ void ds_read_b128(bf16x8 &d, uint32_t addr) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "i"(OFF));
+}
+template <int N>
+__device__ __forceinline__ void wait_lgkm(bf16x8 &a, bf16x8 &b0, bf16x8 &b1, bf16x8 &b2,
+                                          bf16x8 &b3) {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt takes 0..15");
+  asm volatile("s_waitcnt lgkmcnt(%5)"
+               : "+v"(a), "+v"(b0), "+v"(b1), "+v"(b2), "+v"(b3)
+               : "i"(N));
+}
+// wait_lgkm<n> for a count known only after unrolling (the branches fold away).
+template <int N = 15>
+__device__ __forceinline__ void wait_lgkm_n(int n, bf16x8 &a, bf16x8 &b0, bf16x8 &b1, bf16x8 &b2,
+                                            bf16x8 &b3) {
+  if (n == N)
+    wait_lgkm<N>(a, b0, b1, b2, b3);
+  else if constexpr (N > 0)
+    wait_lgkm_n<N - 1>(n, a, b0, b1, b2, b3);
+}
+
 __device__ __forceinline__ uint16_t to_bf16(float x) {
   uint32_t u = __float_as_uint(x);
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
@@ -100,8 +127,29 @@ __global__ __launch_bounds__(kThreads, 1) void linear_skinny_kernel(LinParams P)
   const int fq = lane >> 4;  // which 8 k of the 32
   const int wr = 16 * wave + fr;
 
+  // LDS byte addresses of this lane's fragments in buffer 0: k-step s reads chunk 4 s + fq of
+  // W row wr and of x row fr (x row 16 mb + fr is mb * 16 rows further, an immediate offset);
+  // both rows have r % 16 == fr, so the chunk sits at slot (4 s + fq) ^ fr.
+  uint32_t a_at[KC / 32], b_at[KC / 32];
+#pragma unroll
+  for (int s = 0; s < KC / 32; ++s) {
+    const uint32_t slot = uint32_t(((4 * s + fq) ^ fr) << 4);
+    a_at[s] = lds_addr(&sW[0][0]) + uint32_t(wr * KC * 2) + slot;
+    b_at[s] = lds_addr(&sX[0][0]) + uint32_t(fr * KC * 2) + slot;
+  }
+  bf16x8 a[KC / 32], b[KC / 32][4];
+#pragma unroll
+  for (int s = 0; s < KC / 32; ++s)
+#pragma unroll
+    for (int mb = MB; mb < 4; ++mb) b[s][mb] = bf16x8{};
+
   // Stages 0..2 before the loop; stage st + 3 goes into buffer (st + 3) % 4, last read in
-  // iteration st - 1, after the barrier of iteration st. Each stage is 8 loads per wave.
+  // iteration st - 1, after the barrier of iteration st. Each stage is 8 loads per wave. A stage
+  // is published by each wave's own vmcnt wait (an LDS DMA is counted until its data is in LDS)
+  // followed by a bare s_barrier: __syncthreads' fence would make the compiler wait for every
+  // load in flight, draining the prefetch at each stage. The asm fragment reads keep their place
+  // on either side of the barrier (both have side effects), and they are complete (wait_lgkm)
+  // before the barrier that lets a later stage overwrite their buffer.
 #pragma unroll
   for (int st = 0; st < kRing - 1; ++st)
     if (st < stages) issue_stage(st, st);
@@ -113,22 +161,23 @@ __global__ __launch_bounds__(kThreads, 1) void linear_skinny_kernel(LinParams P)
       __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
     else
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
+    __builtin_amdgcn_s_barrier();
     if (st + kRing - 1 < stages) issue_stage(st + kRing - 1, (st + kRing - 1) % kRing);
-    const uint16_t *tw = sW[st % kRing];
-    const uint16_t *tx = sX[st % kRing];
+    const uint32_t buf = uint32_t(st % kRing) * uint32_t(kStage * 2);
 #pragma unroll
     for (int s = 0; s < KC / 32; ++s) {
-      const int c = 4 * s + fq;
-      const bf16x8 a = __builtin_bit_cast(
-          bf16x8, *reinterpret_cast<const uint4 *>(&tw[wr * KC + ((c ^ (wr & 15)) << 3)]));
+      ds_read_b128<0>(a[s], a_at[s] + buf);
+      ds_read_b128<0>(b[s][0], b_at[s] + buf);
+      if constexpr (MB > 1) ds_read_b128<16 * KC * 2>(b[s][1], b_at[s] + buf);
+      if constexpr (MB > 2) ds_read_b128<32 * KC * 2>(b[s][2], b_at[s] + buf);
+      if constexpr (MB > 3) ds_read_b128<48 * KC * 2>(b[s][3], b_at[s] + buf);
+    }
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const int xr = 16 * mb + fr;
-        const bf16x8 b = __builtin_bit_cast(
-            bf16x8, *reinterpret_cast<const uint4 *>(&tx[xr * KC + ((c ^ (xr & 15)) << 3)]));
-        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[mb], 0, 0, 0);
-      }
+    for (int s = 0; s < KC / 32; ++s) {
+      wait_lgkm_n((KC / 32 - 1 - s) * (1 + MB), a[s], b[s][0], b[s][1], b[s][2], b[s][3]);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s], b[s][mb], acc[mb], 0, 0, 0);
     }
   }
 

@@ -102,17 +102,28 @@ class AttentionLayerSpec:
 # -----------------------------------------------------------------------------------------------
 # Components
 # -----------------------------------------------------------------------------------------------
+def _product(x, w, skinny):
+    """x . w^T: the decode-sized HIP kernel when asked for and the shapes suit it, else
+    F.linear (the reference's call, modelcore/components/linear.py:14)."""
+    if skinny:
+        from modelcore_amd.kernels import linear as lin
+        if lin.supported(x, w):
+            return lin.linear_bf16(x, w)
+    return F.linear(x, w)
+
+
 class Linear(nn.Linear):
     """fp32 master weight, cast to the activation dtype at every call -- or, after
     ``Model.cache_inference_weights``, read from a copy cast once (the same values, without the
     per-call cast traffic)."""
     _cast = None
+    skinny = False  # set by Model.use_skinny_gemm
 
     def forward(self, x):
         w = self._cast
         if w is None or w.dtype != x.dtype:
             w = self.weight.to(dtype=x.dtype)
-        return F.linear(x, w)
+        return _product(x, w, self.skinny)
 
 
 class RMSNorm(nn.Module):
@@ -297,7 +308,7 @@ class Attention(nn.Module):
         B, T, _ = x.size()
         Hq, Hk, D = self.n_head * self.head_dim, self.n_kv_head * self.head_dim, self.head_dim
         if self._qkv is not None and self._qkv.dtype == x.dtype:
-            qkv = F.linear(x, self._qkv)
+            qkv = _product(x, self._qkv, self.c_q.skinny)
             q = qkv[..., :Hq].view(B, T, self.n_head, D)
             k = qkv[..., Hq:Hq + Hk].view(B, T, self.n_kv_head, D)
             v = qkv[..., Hq + Hk:].view(B, T, self.n_kv_head, D)
@@ -383,7 +394,8 @@ class GatedMLP(nn.Module):
 
     def forward(self, x):
         if self._gate_up is not None and self._gate_up.dtype == x.dtype:
-            gate, up = F.linear(x, self._gate_up).split(self.hidden_dim, dim=-1)
+            gate, up = _product(x, self._gate_up, self.gate_proj.skinny).split(self.hidden_dim,
+                                                                              dim=-1)
             return self.down_proj(self.act(gate) * up)
         return self.down_proj(self.act(self.gate_proj(x)) * self.up_proj(x))
 
@@ -603,6 +615,13 @@ class Model(nn.Module):
                 m._qkv = None
             elif isinstance(m, GatedMLP):
                 m._gate_up = None
+
+    def use_skinny_gemm(self, enabled: bool):
+        """Run the projections of decode-sized batches (at most 64 rows, bf16 cached weights)
+        through ``mcamd_linear_bf16`` instead of F.linear; other shapes keep F.linear."""
+        for m in self.modules():
+            if isinstance(m, Linear):
+                m.skinny = bool(enabled)
 
     def set_fused_epilogue(self, enabled: bool):
         """Choose, for every attention layer at once, between the fused pre-attention launch

@@ -217,6 +217,30 @@ def test_cached_inference_weights_give_identical_logits():
     assert err <= 0.05
 
 
+def test_skinny_gemm_projections_match_the_library_gemm(monkeypatch):
+    """With use_skinny_gemm, a decode-sized forward (32 rows) runs its projections through
+    mcamd_linear_bf16; the logits match the F.linear ones up to the GEMMs' summation order."""
+    from modelcore_amd.kernels import linear as lin
+    cfg = mixed_window_config(n_layer=2)
+    mgr = gpu_manager(torch.bfloat16)
+    model = awake(mgr.create_model(cfg, device=DEV, seed=0))
+    idx = torch.randint(0, cfg.vocab_size, (2, 16), generator=torch.Generator().manual_seed(4)).to(DEV)
+    calls = []
+    real = lin.linear_bf16
+    monkeypatch.setattr(lin, "linear_bf16", lambda *a, **k: (calls.append(1), real(*a, **k))[1])
+    with torch.no_grad():
+        model.cache_inference_weights()
+        a = model(idx)
+        assert not calls
+        model.use_skinny_gemm(True)
+        b = model(idx)
+        model.use_skinny_gemm(False)
+    assert len(calls) >= 4 * 2  # qkv, c_proj, gate/up, down of both layers (+ lm_head)
+    err = (a.float() - b.float()).abs().max().item()
+    print(f"skinny GEMM projections: logits max-abs {err:.4f}", flush=True)
+    assert err <= 0.05
+
+
 def test_fused_pre_attention_step_matches_the_separate_ops():
     """The same bf16 mixed-window, KV-sharing stack with the fused RoPE + QK-norm + x1.2 + append
     launch (the default) and with the reference's separate ops, fed the same tokens (a prefill,
