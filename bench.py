@@ -42,8 +42,9 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
-    ap.add_argument("--skinny-gemm", action="store_true",
-                    help="sample workload: run the decode projections through mcamd_linear_bf16")
+    ap.add_argument("--library-gemm", action="store_true",
+                    help="sample workload: run the decode projections through F.linear (the "
+                         "library GEMM) instead of mcamd_linear_bf16")
     ap.add_argument("--workload", choices=("decode", "prefill", "replicate", "mixed", "sample"),
                     default="decode",
                     help="decode: the decode microbench (default, the headline metric); prefill: "
@@ -400,7 +401,7 @@ def bench_sample(args):
     log(f"building the {SM_LAYERS}-layer model on the GPU (seed 0)")
     model = mgr.create_model(cfg, device=dev, seed=0)
     model.cache_inference_weights()
-    model.use_skinny_gemm(args.skinny_gemm)
+    model.use_skinny_gemm(not args.library_gemm)
     prompt = torch.randint(0, SM_V, (SM_PROMPT,), generator=torch.Generator().manual_seed(0))
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -450,6 +451,7 @@ def bench_sample(args):
                    "layers": SM_LAYERS, "d_model": SM_D, "n_head": SM_H, "n_kv_head": SM_HKV,
                    "head_dim": D, "mlp_hidden": SM_HID, "vocab": SM_V, "rows": SM_ROWS,
                    "prompt": SM_PROMPT, "new_tokens": SM_NEW,
+                   "decode_gemm": "F.linear" if args.library_gemm else "mcamd_linear_bf16",
                    "prefill_and_replicate_ms": round(prefill_ms, 2)},
         "roofline": {"kernel": "whole decode step (bf16 weight GEMMs + cached attention of 32 "
                                "layers + sampling)", "bound": "hbm", "achieved": round(gbps, 1),

@@ -48,9 +48,12 @@ def _token_rows(t: torch.Tensor) -> tuple[torch.Tensor, int]:
     """t (B, T, heads, D) with heads and D contiguous and tokens evenly strided (a view of a fused
     projection's output qualifies), and the token stride in elements; else a contiguous copy."""
     B, T, Hh, D = t.shape
-    if t.stride(3) == 1 and t.stride(2) == D and t.stride(0) == T * t.stride(1) \
-            and t.stride(1) >= Hh * D:
-        return t, t.stride(1)
+    # With one token per row its stride is meaningless (torch's views give the size-1 dim any
+    # stride): tokens are then rows, stride(0) apart.
+    tok = t.stride(1) if T > 1 else t.stride(0)
+    if t.stride(3) == 1 and t.stride(2) == D and (B == 1 or t.stride(0) == T * tok) \
+            and tok >= Hh * D:
+        return t, tok
     t = t.contiguous()
     return t, Hh * D
 

@@ -130,3 +130,21 @@ def test_a_planted_sign_error_is_caught(monkeypatch):
         test_oracle_equals_the_harness_composition(torch.float32, False)
     with pytest.raises(AssertionError):
         test_rotation_runs_by_minus_theta()
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_views_of_a_fused_projection_are_taken_in_place(T):
+    """q/k/v views of a (B, T, H*D + 2*H_kv*D) projection reach the kernel without a copy, one
+    token per row (a decode step, where torch gives the size-1 token dim an arbitrary stride)
+    included; their token stride is the projection's row width."""
+    from modelcore_amd.kernels.qk_epilogue import _token_rows
+    B, H, H_kv, D = 4, 8, 2, 16
+    n = (H + 2 * H_kv) * D
+    qkv = torch.zeros(B, T, n)
+    for lo, heads in ((0, H), (H * D, H_kv), ((H + H_kv) * D, H_kv)):
+        view = qkv[..., lo:lo + heads * D].view(B, T, heads, D)
+        t, stride = _token_rows(view)
+        assert t.data_ptr() == view.data_ptr() and stride == n
+    c = torch.zeros(B, T, H, D).transpose(0, 1)  # rows not evenly strided: copied
+    t, stride = _token_rows(c)
+    assert t.is_contiguous() and stride == H * D

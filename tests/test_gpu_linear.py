@@ -32,7 +32,7 @@ def _check(y, x, w):
 
 SHAPES = [(1, 1024, 512), (7, 4096, 4096), (33, 1024, 1536), (64, 14336, 4096),
           (64, 4096, 14336), (32, 6144, 4096), (64, 32768, 1024), (48, 28672, 4096),
-          (16, 4096, 4096)]
+          (16, 4096, 4096), (20, 24640, 512)]  # the last: 128-row tiles, the last one half full
 
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
