@@ -45,6 +45,9 @@ def parse_args():
     ap.add_argument("--library-gemm", action="store_true",
                     help="sample workload: run the decode projections through F.linear (the "
                          "library GEMM) instead of mcamd_linear_bf16")
+    ap.add_argument("--separate-residual", action="store_true",
+                    help="sample workload: run each residual add and RMS-norm as torch's separate "
+                         "ops instead of one mcamd_residual_rmsnorm launch")
     ap.add_argument("--workload", choices=("decode", "prefill", "replicate", "mixed", "sample"),
                     default="decode",
                     help="decode: the decode microbench (default, the headline metric); prefill: "
@@ -402,6 +405,7 @@ def bench_sample(args):
     model = mgr.create_model(cfg, device=dev, seed=0)
     model.cache_inference_weights()
     model.use_skinny_gemm(not args.library_gemm)
+    model.set_fused_residual(not args.separate_residual)
     prompt = torch.randint(0, SM_V, (SM_PROMPT,), generator=torch.Generator().manual_seed(0))
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -452,6 +456,8 @@ def bench_sample(args):
                    "head_dim": D, "mlp_hidden": SM_HID, "vocab": SM_V, "rows": SM_ROWS,
                    "prompt": SM_PROMPT, "new_tokens": SM_NEW,
                    "decode_gemm": "F.linear" if args.library_gemm else "mcamd_linear_bf16",
+                   "residual_step": "torch add + F.rms_norm" if args.separate_residual
+                   else "mcamd_residual_rmsnorm",
                    "prefill_and_replicate_ms": round(prefill_ms, 2)},
         "roofline": {"kernel": "whole decode step (bf16 weight GEMMs + cached attention of 32 "
                                "layers + sampling)", "bound": "hbm", "achieved": round(gbps, 1),

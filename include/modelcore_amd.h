@@ -178,6 +178,32 @@ int mcamd_linear_bf16(const void *x, int64_t ldx, const void *w, void *y, int64_
                       int64_t n, int64_t k, int64_t k_splits, void *workspace,
                       size_t workspace_bytes, void *stream);
 
+/*
+ * mcamd_linear_bf16 without the sum: the K-split partial products, written to `part` as
+ * (k_splits, m, n) fp32 (k_splits = 1 included), for a consumer that sums them itself in the
+ * same order (mcamd_residual_rmsnorm). Same shape rules as mcamd_linear_bf16; part 16-byte
+ * aligned, k_splits * m * n floats. Replaces the same F.linear call sites (c_proj and down_proj
+ * in the reference, modelcore/components/attention.py:183, modelcore/components/mlp.py:90), with
+ * the reduction left to the fused residual step below.
+ */
+int mcamd_linear_bf16_partials(const void *x, int64_t ldx, const void *w, float *part, int64_t m,
+                               int64_t n, int64_t k, int64_t k_splits, void *stream);
+
+/*
+ * The residual update and the next RMS-norm, fused, for (m, n) bf16 rows (contiguous, n a
+ * multiple of 8):
+ *   y     = bf16(sum_s part[s])  (part: (splits, m, n) fp32, summed in order s = 0, 1, ...),
+ *           or y given in bf16 (part = NULL)
+ *   x_out = bf16(x + y)
+ *   h_out = bf16(x_out * rsqrt(mean(x_out^2) + eps))   (fp32 arithmetic)
+ * Replaces, in a block (modelcore/components/block.py:54-60), the residual add `x + f(norm(x))`
+ * and the RMSNorm that follows it (modelcore/components/norm.py:43-44), plus the split-K sum of
+ * the projection that produced f.
+ */
+int mcamd_residual_rmsnorm(const void *x, const float *part, int64_t splits, const void *y,
+                           void *x_out, void *h_out, int64_t m, int64_t n, float eps,
+                           void *stream);
+
 #ifdef __cplusplus
 }
 #endif

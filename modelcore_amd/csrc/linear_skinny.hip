@@ -44,9 +44,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 struct LinParams {
   const uint16_t *x, *w;
   uint16_t *y;
-  float *part;  // [S][M][N] fp32 partials when S > 1
+  float *part;  // [S][M][N] fp32 partials when S > 1 or raw
   int64_t ldx, ldy;
   int M, N, K, S;
+  int raw;      // write the partials (fp32) even for S = 1, and leave the sum to the consumer
 };
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void linear_skinny_kernel(LinParams 
   for (int mb = 0; mb < MB; ++mb) {
     const int m = 16 * mb + fr;
     if (m >= P.M) continue;
-    if (P.S == 1) {
+    if (P.S == 1 && !P.raw) {
       const uint32_t lo = uint32_t(to_bf16(acc[mb][0])) | (uint32_t(to_bf16(acc[mb][1])) << 16);
       const uint32_t hi = uint32_t(to_bf16(acc[mb][2])) | (uint32_t(to_bf16(acc[mb][3])) << 16);
       *reinterpret_cast<uint2 *>(P.y + int64_t(m) * P.ldy + n) = uint2{lo, hi};
@@ -258,9 +259,11 @@ extern "C" size_t mcamd_linear_bf16_workspace_bytes(int64_t m, int64_t n, int64_
   return k_splits > 1 ? size_t(k_splits) * size_t(m) * size_t(n) * sizeof(float) : 0;
 }
 
-extern "C" int mcamd_linear_bf16(const void *x, int64_t ldx, const void *w, void *y, int64_t ldy,
-                                 int64_t m, int64_t n, int64_t k, int64_t k_splits,
-                                 void *workspace, size_t workspace_bytes, void *stream) {
+namespace {
+
+// Argument checks shared by the two entry points; fills P on success.
+int check_linear(const void *x, int64_t ldx, const void *w, int64_t m, int64_t n, int64_t k,
+                 int64_t k_splits, LinParams &P) {
   if (m < 0 || m > 64)
     return fail(MCAMD_EUNSUPPORTED, "linear_bf16: m must be at most 64 (decode-sized batches)");
   if (k_splits < 1 || k_splits > 64)
@@ -270,44 +273,82 @@ extern "C" int mcamd_linear_bf16(const void *x, int64_t ldx, const void *w, void
                 "linear_bf16: n must be a multiple of 64 and k of 128 * k_splits");
   if (n > (int64_t(1) << 30) || int64_t(128) * k * 2 >= (int64_t(1) << 31))
     return fail(MCAMD_EUNSUPPORTED, "linear_bf16: n or k too large");
-  if (m == 0) {
-    clear_error();
-    return MCAMD_OK;
+  if (m > 0) {
+    if (!x || !w) return fail(MCAMD_EINVAL, "linear_bf16: null pointer");
+    if (ldx < k || ldx % 8 != 0)
+      return fail(MCAMD_EINVAL, "linear_bf16: need ldx >= k, a multiple of 8");
+    if (kXRows * ldx * 2 >= (int64_t(1) << 31))
+      return fail(MCAMD_EUNSUPPORTED, "linear_bf16: activations too large");
+    if (!aligned(x, 16) || !aligned(w, 16))
+      return fail(MCAMD_EINVAL, "linear_bf16: x and w must be 16-byte aligned");
   }
-  if (!x || !w || !y) return fail(MCAMD_EINVAL, "linear_bf16: null pointer");
-  if (ldx < k || ldy < n || ldy % 4 != 0 || ldx % 8 != 0)
-    return fail(MCAMD_EINVAL, "linear_bf16: need ldx >= k (a multiple of 8), ldy >= n (of 4)");
-  if (kXRows * ldx * 2 >= (int64_t(1) << 31))
-    return fail(MCAMD_EUNSUPPORTED, "linear_bf16: activations too large");
-  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 8))
-    return fail(MCAMD_EINVAL, "linear_bf16: x and w must be 16-byte aligned, y 8-byte aligned");
-  if (k_splits > 1 &&
-      (!workspace || workspace_bytes < mcamd_linear_bf16_workspace_bytes(m, n, k_splits) ||
-       !aligned(workspace, 16)))
-    return fail(MCAMD_EWORKSPACE, "linear_bf16: workspace missing or too small for k_splits");
-  LinParams P;
+  P = LinParams{};
   P.x = static_cast<const uint16_t *>(x);
   P.w = static_cast<const uint16_t *>(w);
-  P.y = static_cast<uint16_t *>(y);
-  P.part = static_cast<float *>(workspace);
   P.ldx = ldx;
-  P.ldy = ldy;
   P.M = int(m);
   P.N = int(n);
   P.K = int(k);
   P.S = int(k_splits);
-  hipStream_t s = as_stream(stream);
+  return MCAMD_OK;
+}
+
+void launch_linear(const LinParams &P, hipStream_t s) {
   // Eight waves where 128-row tiles alone fill the GPU and the activation tile is large enough
   // for its traffic to matter (measured on MI355X, cold weights, 28672 x 4096: 64 rows 49.2 us
   // against 57.6 with four waves; 16 rows 49.2 against 47.3); four waves otherwise.
-  if (k_splits == 1 && n >= 192 * 128 && m > 16)
+  if (P.S == 1 && P.N >= 192 * 128 && P.M > 16)
     launch_skinny<8>(P, s);
   else
     launch_skinny<4>(P, s);
-  int st = launch_status("linear_bf16");
+}
+
+}  // namespace
+
+extern "C" int mcamd_linear_bf16(const void *x, int64_t ldx, const void *w, void *y, int64_t ldy,
+                                 int64_t m, int64_t n, int64_t k, int64_t k_splits,
+                                 void *workspace, size_t workspace_bytes, void *stream) {
+  LinParams P;
+  int st = check_linear(x, ldx, w, m, n, k, k_splits, P);
+  if (st != MCAMD_OK) return st;
+  if (m == 0) {
+    clear_error();
+    return MCAMD_OK;
+  }
+  if (!y) return fail(MCAMD_EINVAL, "linear_bf16: null pointer");
+  if (ldy < n || ldy % 4 != 0 || !aligned(y, 8))
+    return fail(MCAMD_EINVAL, "linear_bf16: need ldy >= n (a multiple of 4), y 8-byte aligned");
+  if (k_splits > 1 &&
+      (!workspace || workspace_bytes < mcamd_linear_bf16_workspace_bytes(m, n, k_splits) ||
+       !aligned(workspace, 16)))
+    return fail(MCAMD_EWORKSPACE, "linear_bf16: workspace missing or too small for k_splits");
+  P.y = static_cast<uint16_t *>(y);
+  P.ldy = ldy;
+  P.part = static_cast<float *>(workspace);
+  hipStream_t s = as_stream(stream);
+  launch_linear(P, s);
+  st = launch_status("linear_bf16");
   if (st != MCAMD_OK || k_splits == 1) return st;
   const int64_t quads = m * (n / 4);
   hipLaunchKernelGGL(linear_reduce_kernel, dim3(unsigned((quads + 255) / 256)), dim3(256), 0, s,
                      P);
   return launch_status("linear_bf16 reduce");
+}
+
+extern "C" int mcamd_linear_bf16_partials(const void *x, int64_t ldx, const void *w, float *part,
+                                          int64_t m, int64_t n, int64_t k, int64_t k_splits,
+                                          void *stream) {
+  LinParams P;
+  int st = check_linear(x, ldx, w, m, n, k, k_splits, P);
+  if (st != MCAMD_OK) return st;
+  if (m == 0) {
+    clear_error();
+    return MCAMD_OK;
+  }
+  if (!part || !aligned(part, 16))
+    return fail(MCAMD_EINVAL, "linear_bf16_partials: part must be a 16-byte aligned buffer");
+  P.part = part;
+  P.raw = 1;
+  launch_linear(P, as_stream(stream));
+  return launch_status("linear_bf16_partials");
 }

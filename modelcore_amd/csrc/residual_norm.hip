@@ -1,0 +1,133 @@
+// The residual update and the RMS-norm after a projection, fused, for decode-sized batches:
+//   y      = bf16(sum over s of part[s][m][:])        (the K-split partials of the projection, in
+//                                                     order; or y given in bf16)
+//   x_out  = bf16(x + y)                               (the residual stream, `x = x + f(norm(x))`)
+//   h_out  = bf16(x_out * rsqrt(mean(x_out^2) + eps))  (the next norm, fp32 arithmetic)
+// Replaces, per block of the reference (modelcore/components/block.py:54-60), the split-K reduce
+// of the projection, the residual add and the following RMSNorm (modelcore/components/norm.py:
+// 43-44, F.rms_norm): three launches become one, and h_out feeds the next projection (or the
+// next block's mixer, or the lm_head) directly.
+//
+// One workgroup of 256 threads per row m; each thread owns chunks of 8 elements (16 bytes of
+// bf16, 32 of fp32 partials), so every load and store is a full 16-byte vector. The mean square
+// is a wave sum (DPP/shuffles) then a sum over the four waves through LDS.
+#include "kernels.h"
+
+namespace mcamd {
+namespace {
+
+constexpr int kThreads = 256;
+
+struct ResParams {
+  const uint16_t *x, *y;
+  const float *part;
+  uint16_t *x_out, *h_out;
+  int M, N, S;
+  float eps;
+};
+
+__device__ __forceinline__ uint16_t to_bf16(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+__device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+__device__ __forceinline__ void unpack8(const uint4 &u, float (&v)[8]) {
+  v[0] = bf16_lo(u.x), v[1] = bf16_hi(u.x), v[2] = bf16_lo(u.y), v[3] = bf16_hi(u.y);
+  v[4] = bf16_lo(u.z), v[5] = bf16_hi(u.z), v[6] = bf16_lo(u.w), v[7] = bf16_hi(u.w);
+}
+__device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
+  return uint4{uint32_t(to_bf16(v[0])) | (uint32_t(to_bf16(v[1])) << 16),
+               uint32_t(to_bf16(v[2])) | (uint32_t(to_bf16(v[3])) << 16),
+               uint32_t(to_bf16(v[4])) | (uint32_t(to_bf16(v[5])) << 16),
+               uint32_t(to_bf16(v[6])) | (uint32_t(to_bf16(v[7])) << 16)};
+}
+
+__global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(ResParams P) {
+  __shared__ float wsum[kThreads / 64];
+  const int m = blockIdx.x;
+  const int chunks = P.N / 8;
+  const int64_t row = int64_t(m) * P.N;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < chunks; c += kThreads) {
+    float xv[8], yv[8];
+    unpack8(*reinterpret_cast<const uint4 *>(P.x + row + 8 * c), xv);
+    if (P.part) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < P.S; ++s) {
+        const float4 *p = reinterpret_cast<const float4 *>(P.part + int64_t(s) * P.M * P.N + row +
+                                                           8 * c);
+        const float4 a = p[0], b = p[1];
+        acc[0] += a.x, acc[1] += a.y, acc[2] += a.z, acc[3] += a.w;
+        acc[4] += b.x, acc[5] += b.y, acc[6] += b.z, acc[7] += b.w;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) yv[i] = __uint_as_float(uint32_t(to_bf16(acc[i])) << 16);
+    } else {
+      unpack8(*reinterpret_cast<const uint4 *>(P.y + row + 8 * c), yv);
+    }
+    float sv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      sv[i] = __uint_as_float(uint32_t(to_bf16(xv[i] + yv[i])) << 16);
+      ss = fmaf(sv[i], sv[i], ss);
+    }
+    *reinterpret_cast<uint4 *>(P.x_out + row + 8 * c) = pack8(sv);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) total += wsum[w];
+  const float r = rsqrtf(total / float(P.N) + P.eps);
+  // Second pass over this thread's own chunks of x_out (its own writes, still in its cache).
+  for (int c = threadIdx.x; c < chunks; c += kThreads) {
+    float sv[8];
+    unpack8(*reinterpret_cast<const uint4 *>(P.x_out + row + 8 * c), sv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sv[i] *= r;
+    *reinterpret_cast<uint4 *>(P.h_out + row + 8 * c) = pack8(sv);
+  }
+}
+
+}  // namespace
+}  // namespace mcamd
+
+using namespace mcamd;
+
+extern "C" int mcamd_residual_rmsnorm(const void *x, const float *part, int64_t splits,
+                                      const void *y, void *x_out, void *h_out, int64_t m,
+                                      int64_t n, float eps, void *stream) {
+  if (m < 0 || n <= 0 || n % 8 != 0 || m > (int64_t(1) << 31) - 1 || m * n >= (int64_t(1) << 40))
+    return fail(MCAMD_EINVAL, "residual_rmsnorm: need m >= 0 and n > 0 a multiple of 8");
+  if ((part == nullptr) == (y == nullptr))
+    return fail(MCAMD_EINVAL, "residual_rmsnorm: pass the partials or y, not both");
+  if (part && (splits < 1 || splits > 64))
+    return fail(MCAMD_EINVAL, "residual_rmsnorm: splits must be in [1, 64]");
+  if (!(eps >= 0.f)) return fail(MCAMD_EINVAL, "residual_rmsnorm: eps must be >= 0");
+  if (m == 0) {
+    clear_error();
+    return MCAMD_OK;
+  }
+  if (!x || !x_out || !h_out) return fail(MCAMD_EINVAL, "residual_rmsnorm: null pointer");
+  if (!aligned(x, 16) || !aligned(x_out, 16) || !aligned(h_out, 16) ||
+      (part && !aligned(part, 16)) || (y && !aligned(y, 16)))
+    return fail(MCAMD_EINVAL, "residual_rmsnorm: buffers must be 16-byte aligned");
+  ResParams P;
+  P.x = static_cast<const uint16_t *>(x);
+  P.y = static_cast<const uint16_t *>(y);
+  P.part = part;
+  P.x_out = static_cast<uint16_t *>(x_out);
+  P.h_out = static_cast<uint16_t *>(h_out);
+  P.M = int(m);
+  P.N = int(n);
+  P.S = part ? int(splits) : 0;
+  P.eps = eps;
+  hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(unsigned(m)), dim3(kThreads), 0,
+                     as_stream(stream), P);
+  return launch_status("residual_rmsnorm");
+}

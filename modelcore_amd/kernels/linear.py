@@ -14,7 +14,7 @@ import torch
 
 from modelcore_amd import _ext
 
-__all__ = ["supported", "linear_bf16", "k_splits"]
+__all__ = ["supported", "linear_bf16", "linear_bf16_partials", "Partials", "k_splits"]
 
 MAX_ROWS = 64
 TILE_N = 64     # rows of W per workgroup (four waves)
@@ -86,3 +86,33 @@ def linear_bf16(x: torch.Tensor, w: torch.Tensor, splits: int | None = None) -> 
                                ws.numel() if ws is not None else 0, _ext.stream_handle(x.device))
     _ext.check(st, "linear_bf16")
     return y.view(*x.shape[:-1], n)
+
+
+class Partials:
+    """The K-split partial products of x . W^T, unsummed: ``part`` is (splits, rows, n) fp32 and
+    ``shape`` the shape the summed product would have. Only a consumer that sums them itself
+    takes one (``kernels.residual.residual_rmsnorm``)."""
+    __slots__ = ("part", "splits", "shape")
+
+    def __init__(self, part: torch.Tensor, splits: int, shape: tuple):
+        self.part, self.splits, self.shape = part, splits, shape
+
+
+def linear_bf16_partials(x: torch.Tensor, w: torch.Tensor, splits: int | None = None) -> Partials:
+    """``linear_bf16(x, w)`` with the sum of its K-split partials left to the consumer."""
+    _ext.require_rocm(x, w, what="linear_bf16_partials")
+    if not supported(x, w):
+        raise ValueError(f"linear_bf16_partials takes what linear_bf16 takes; got x "
+                         f"{tuple(x.shape)} {x.dtype}, w {tuple(w.shape)} {w.dtype}")
+    n, k = w.shape
+    x2 = x.reshape(-1, k)
+    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    s = splits if splits is not None else k_splits(m, n, k)
+    part = torch.empty(s, m, n, dtype=torch.float32, device=x.device)
+    st = _ext.lib().mcamd_linear_bf16_partials(x2.data_ptr(), x2.stride(0), w.data_ptr(),
+                                               part.data_ptr(), m, n, k, s,
+                                               _ext.stream_handle(x.device))
+    _ext.check(st, "linear_bf16_partials")
+    return Partials(part, s, (*x.shape[:-1], n))

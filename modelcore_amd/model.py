@@ -102,13 +102,14 @@ class AttentionLayerSpec:
 # -----------------------------------------------------------------------------------------------
 # Components
 # -----------------------------------------------------------------------------------------------
-def _product(x, w, skinny):
-    """x . w^T: the decode-sized HIP kernel when asked for and the shapes suit it, else
-    F.linear (the reference's call, modelcore/components/linear.py:14)."""
+def _product(x, w, skinny, partial=False):
+    """x . w^T: the decode-sized HIP kernel when asked for and the shapes suit it (with
+    ``partial``, its unsummed K-split partials, for a consumer that sums them), else F.linear
+    (the reference's call, modelcore/components/linear.py:14)."""
     if skinny:
         from modelcore_amd.kernels import linear as lin
         if lin.supported(x, w):
-            return lin.linear_bf16(x, w)
+            return lin.linear_bf16_partials(x, w) if partial else lin.linear_bf16(x, w)
     return F.linear(x, w)
 
 
@@ -118,12 +119,13 @@ class Linear(nn.Linear):
     per-call cast traffic)."""
     _cast = None
     skinny = False  # set by Model.use_skinny_gemm
+    partial = False  # set by Model.set_fused_residual: may return the product's partials
 
     def forward(self, x):
         w = self._cast
         if w is None or w.dtype != x.dtype:
             w = self.weight.to(dtype=x.dtype)
-        return _product(x, w, self.skinny)
+        return _product(x, w, self.skinny, self.partial)
 
 
 class RMSNorm(nn.Module):
@@ -436,9 +438,29 @@ class Block(nn.Module):
         self.mixer.init_weights()
         self.ffn.init_weights()
 
+    fuse_residual = False  # set by Model.set_fused_residual
+
     def forward(self, x, kv_cache, kv_bus):
         x = x + self.mixer(self.norm(x), kv_cache, kv_bus)
         return x + self.ffn(self.norm(x))
+
+    def forward_carry(self, x, h, kv_cache, kv_bus):
+        """forward(), also returning norm(x) of its output, which the next block's mixer (or the
+        lm_head) takes as is; h = norm(x) of the input when the previous block made it. Each
+        residual add and the norm after it run as one launch (residual_rmsnorm), which also sums
+        the K-split partials of the projection before it."""
+        if h is None:
+            h = self.norm(x)
+        x, h = self._residual(x, self.mixer(h, kv_cache, kv_bus))
+        return self._residual(x, self.ffn(h))
+
+    def _residual(self, x, f):
+        from modelcore_amd.kernels import residual
+        from modelcore_amd.kernels.linear import Partials
+        if isinstance(f, Partials) or residual.supported(x) and x.numel() // x.shape[-1] <= 64:
+            return residual.residual_rmsnorm(x, f, self.norm.eps)
+        x = x + f
+        return x, self.norm(x)
 
 
 class Stack(nn.Module):
@@ -454,10 +476,19 @@ class Stack(nn.Module):
             block.init_weights()
 
     def forward(self, x, kv_cache):
+        return self.forward_carry(x, kv_cache)[0]
+
+    def forward_carry(self, x, kv_cache):
+        """The layer loop, also returning norm(x) of the output when the last block made it
+        (blocks with fused residual steps), else None."""
         kv_bus = {}
+        h = None
         for block in self.blocks:
-            x = block(x, kv_cache, kv_bus)
-        return x
+            if block.fuse_residual:
+                x, h = block.forward_carry(x, h, kv_cache, kv_bus)
+            else:
+                x, h = block(x, kv_cache, kv_bus), None
+        return x, h
 
 
 class TokenEmbedding(nn.Module):
@@ -495,8 +526,9 @@ class LMHead(nn.Module):
     def init_weights(self):
         nn.init.normal_(self.lm_head.weight, mean=0.0, std=0.001)
 
-    def forward(self, x):
-        logits = self.lm_head(self.norm(x))[..., :self.vocab_size].float()
+    def forward(self, x, h=None):
+        """h, when given, is norm(x) already made by the last block."""
+        logits = self.lm_head(self.norm(x) if h is None else h)[..., :self.vocab_size].float()
         if self.softcap is not None:
             logits = self.softcap * torch.tanh(logits / self.softcap)
         return logits
@@ -616,6 +648,20 @@ class Model(nn.Module):
             elif isinstance(m, GatedMLP):
                 m._gate_up = None
 
+    def set_fused_residual(self, enabled: bool):
+        """Run each block's residual adds and the RMS-norms after them as one launch each
+        (residual_rmsnorm), with the norm carried into the next block and the lm_head, and let
+        c_proj / down_proj hand over their unsummed K-split partials when they run on the skinny
+        GEMM. For bf16 decode-sized rows; results differ from the separate ops only in the order
+        of the norm's fp32 sum of squares. Needs the parameterless RMSNorm."""
+        if enabled and not isinstance(self.shared["norm"], RMSNorm):
+            raise NotImplementedError("fused residual steps need the rms_norm shared norm")
+        for block in self.body.blocks:
+            block.fuse_residual = bool(enabled)
+            block.mixer.c_proj.partial = bool(enabled)
+            out = getattr(block.ffn, "down_proj", None) or block.ffn.c_proj
+            out.partial = bool(enabled)
+
     def use_skinny_gemm(self, enabled: bool):
         """Run the projections of decode-sized batches (at most 64 rows, bf16 cached weights)
         through ``mcamd_linear_bf16`` instead of F.linear; other shapes keep F.linear."""
@@ -640,19 +686,21 @@ class Model(nn.Module):
         if targets is not None:
             raise NotImplementedError("training loss is not part of the inference path")
         x = self.embedding(idx)
-        x = self.body(x, kv_cache)
+        x, h = self.body.forward_carry(x, kv_cache)
         if kv_cache is not None:
             kv_cache.advance(idx.size(1))
-        return self.unembedding(x)
+        return self.unembedding(x, h)
 
     def last_logits(self, idx, kv_cache, last):
         """forward(), but the head runs only at position last[b] of row b: (B, vocab) logits.
         The head is per position, so these equal forward()[b, last[b]]; a prompt prefill needs
         only its last position, and skips the (B, T, vocab) logits of all the others."""
-        x = self.body(self.embedding(idx), kv_cache)
+        x, h = self.body.forward_carry(self.embedding(idx), kv_cache)
         kv_cache.advance(idx.size(1))
         rows = torch.arange(idx.size(0), device=x.device)
-        return self.unembedding(x[rows, last.to(x.device)].unsqueeze(1))[:, 0]
+        last = last.to(x.device)
+        return self.unembedding(x[rows, last].unsqueeze(1),
+                                None if h is None else h[rows, last].unsqueeze(1))[:, 0]
 
 
 def kv_cache_spec(layer_specs):

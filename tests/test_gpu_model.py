@@ -272,16 +272,54 @@ def test_fused_pre_attention_step_matches_the_separate_ops():
         assert (a.float() - b.float()).abs().max() <= 0.1
 
 
-def test_captured_decode_step_replays_the_eager_steps():
-    """A whole decode step (forward, device sampling, advance) captured once as a HIP graph and
-    replayed: the same tokens, logits and cache as the same steps run eagerly, and the host-side
-    position kept in step with the device."""
-    from modelcore_amd.sampling import PhiloxSampler
-    _note("captured decode step")
+def test_fused_residual_steps_match_the_separate_ops():
+    """With set_fused_residual (and the skinny GEMM), each residual add + RMS-norm is one launch
+    that also sums c_proj's / down_proj's K-split partials, and the norm is carried to the next
+    block and the lm_head: a prefill (rows > 64: the separate ops) then cached single-token steps
+    (the fused launches) give the logits of the separate ops within bf16 rounding."""
+    _note("fused residual steps")
     cfg = mixed_window_config(n_layer=4)
     mgr = gpu_manager(torch.bfloat16)
     model = awake(mgr.create_model(cfg, device=DEV, seed=0))
     model.cache_inference_weights()
+    model.use_skinny_gemm(True)
+    g = torch.Generator().manual_seed(6)
+    B, P, steps = 4, 60, 6
+    tokens = torch.randint(0, cfg.vocab_size, (B, P + steps), generator=g).to(DEV)
+    runs = []
+    for fused in (True, False):
+        model.set_fused_residual(fused)
+        cache = mgr.new_kv_cache(model, batch_size=B, seq_len=P + steps)
+        with torch.no_grad():
+            logits = [model(tokens[:, :P], kv_cache=cache)[:, -1]]
+            for t in range(P, P + steps):
+                logits.append(model(tokens[:, t:t + 1], kv_cache=cache)[:, -1])
+            last = model.last_logits(tokens[:, :P], mgr.new_kv_cache(model, batch_size=B,
+                                                                     seq_len=P),
+                                     torch.full((B,), P - 1))
+        runs.append((torch.stack(logits).float(), last.float()))
+    model.set_fused_residual(False)
+    (la, lla), (lb, llb) = runs
+    assert torch.equal(la[0], lb[0]) and torch.equal(lla, llb)  # prefill: the separate ops
+    err = (la - lb).abs().max().item()
+    print(f"logits max-abs fused residual vs separate: {err:.4f} (scale "
+          f"{lb.abs().max().item():.3f})", flush=True)
+    assert err <= 0.1
+
+
+@pytest.mark.parametrize("fast", [False, True], ids=["library-gemm", "skinny-fused-residual"])
+def test_captured_decode_step_replays_the_eager_steps(fast):
+    """A whole decode step (forward, device sampling, advance) captured once as a HIP graph and
+    replayed: the same tokens, logits and cache as the same steps run eagerly, and the host-side
+    position kept in step with the device; also with the skinny GEMM and fused residual steps."""
+    from modelcore_amd.sampling import PhiloxSampler
+    _note("captured decode step", fast)
+    cfg = mixed_window_config(n_layer=4)
+    mgr = gpu_manager(torch.bfloat16)
+    model = awake(mgr.create_model(cfg, device=DEV, seed=0))
+    model.cache_inference_weights()
+    model.use_skinny_gemm(fast)
+    model.set_fused_residual(fast)
     prompt = torch.randint(0, cfg.vocab_size, (90,), generator=torch.Generator().manual_seed(5))
     R, n = 6, 10
 
