@@ -437,8 +437,12 @@ def bench_sample(args):
         torch.cuda.synchronize()
     ms = start.elapsed_time(end) / K
     assert dec.kv_cache.get_pos() == SM_PROMPT + SM_NEW
+    # Weights a step reads: every cached Linear copy (QKV copies are views of their stack), and
+    # the interleaved gate/up stacks, whose rows have no per-Linear view.
     weight_bytes = sum(m._cast.numel() * m._cast.element_size() for m in model.modules()
                        if getattr(m, "_cast", None) is not None)
+    weight_bytes += sum(m._gate_up.numel() * m._gate_up.element_size() for m in model.modules()
+                        if getattr(m, "_gate_up_blocked", False))
     kv = sum(stats.decode_step_bytes([SM_PROMPT + W + i] * SM_ROWS, SM_H, SM_HKV, D, 2)
              for i in range(K)) / K * SM_LAYERS
     step_bytes = weight_bytes + kv

@@ -179,6 +179,20 @@ int mcamd_linear_bf16(const void *x, int64_t ldx, const void *w, void *y, int64_
                       size_t workspace_bytes, void *stream);
 
 /*
+ * The gated MLP's first half at decode sizes: with W = [W_gate; W_up] interleaved in blocks of 64
+ * rows (rows 128 b .. 128 b + 63 = gate rows 64 b .. 64 b + 63, the next 64 = the up rows of the
+ * same units; W is (2 hidden, k)), writes h (m, hidden) bf16, rows `ldh` apart:
+ *   h[r][j] = bf16(bf16(act(g)) * u),  g = bf16(x[r] . W_gate[j]),  u = bf16(x[r] . W_up[j])
+ * in fp32 arithmetic, i.e. torch's `act(gate(x)) * up(x)` on bf16 tensors. act = MCAMD_ACT_SILU
+ * (x / (1 + e^-x)); hidden a multiple of 64, k of 128, m <= 64. Replaces GatedMLP.forward's
+ * gate_proj, up_proj and the activation product (modelcore/components/mlp.py:89-90) before
+ * down_proj.
+ */
+enum { MCAMD_ACT_SILU = 0 };
+int mcamd_linear_bf16_gated(const void *x, int64_t ldx, const void *w, void *h, int64_t ldh,
+                            int64_t m, int64_t hidden, int64_t k, int act, void *stream);
+
+/*
  * mcamd_linear_bf16 without the sum: the K-split partial products, written to `part` as
  * (k_splits, m, n) fp32 (k_splits = 1 included), for a consumer that sums them itself in the
  * same order (mcamd_residual_rmsnorm). Same shape rules as mcamd_linear_bf16; part 16-byte

@@ -48,6 +48,7 @@ struct LinParams {
   int64_t ldx, ldy;
   int M, N, K, S;
   int raw;      // write the partials (fp32) even for S = 1, and leave the sum to the consumer
+  int gated;    // W holds [gate; up] interleaved in 64-row blocks: write silu(gate) * up to y
 };
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
@@ -89,6 +90,15 @@ __device__ __forceinline__ uint16_t to_bf16(float x) {
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
   u += 0x7fffu + ((u >> 16) & 1u);
   return uint16_t(u >> 16);
+}
+__device__ __forceinline__ float round_bf16(float x) { return __uint_as_float(uint32_t(to_bf16(x)) << 16); }
+
+// h = silu(gate) * up as torch computes it on bf16 tensors: the product's outputs rounded to
+// bf16, silu in fp32 rounded to bf16, the product in fp32 rounded to bf16.
+__device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
+  const float g = round_bf16(gate), u = round_bf16(up);
+  const float a = round_bf16(g / (1.f + expf(-g)));
+  return to_bf16(a * u);
 }
 
 template <int WAVES, int MB>  // MB blocks of 16 activation rows: M <= 16 MB
@@ -206,6 +216,37 @@ __global__ __launch_bounds__(64 * WAVES, 1) void linear_skinny_kernel(LinParams 
   }
 
   // acc[mb][i] = y[m = 16 mb + l % 16][n = n0 + 16 w + 4 (l / 16) + i].
+  if constexpr (WAVES == 8) {
+    if (P.gated) {
+      // Rows 0..63 of the tile are gate rows j, rows 64..127 the up rows of the same j: wave
+      // w + 4 holds, lane for lane, the up values of wave w's gate values. They pass through
+      // LDS (the W ring, free once every wave is past its last stage: a full __syncthreads, so
+      // that no store below can be moved above it).
+      float *xch = reinterpret_cast<float *>(&sW[0][0]);
+      __syncthreads();
+      if (wave >= 4) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xch[(((wave - 4) * MB + mb) * 4 + i) * 64 + lane] = acc[mb][i];
+      }
+      __syncthreads();
+      if (wave >= 4) return;
+      const int j = blockIdx.x * 64 + 16 * wave + 4 * fq;  // hidden unit of acc[.][0]
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int m = 16 * mb + fr;
+        if (m >= P.M) continue;
+        uint16_t hv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          hv[i] = silu_mul_bf16(acc[mb][i], xch[((wave * MB + mb) * 4 + i) * 64 + lane]);
+        *reinterpret_cast<uint2 *>(P.y + int64_t(m) * P.ldy + j) =
+            uint2{uint32_t(hv[0]) | (uint32_t(hv[1]) << 16), uint32_t(hv[2]) | (uint32_t(hv[3]) << 16)};
+      }
+      return;
+    }
+  }
   const int n = n0 + 16 * wave + 4 * fq;
   if (n >= P.N) return;
 #pragma unroll
@@ -333,6 +374,29 @@ extern "C" int mcamd_linear_bf16(const void *x, int64_t ldx, const void *w, void
   hipLaunchKernelGGL(linear_reduce_kernel, dim3(unsigned((quads + 255) / 256)), dim3(256), 0, s,
                      P);
   return launch_status("linear_bf16 reduce");
+}
+
+extern "C" int mcamd_linear_bf16_gated(const void *x, int64_t ldx, const void *w, void *h,
+                                       int64_t ldh, int64_t m, int64_t hidden, int64_t k, int act,
+                                       void *stream) {
+  if (act != MCAMD_ACT_SILU)
+    return fail(MCAMD_EUNSUPPORTED, "linear_bf16_gated: only silu is supported");
+  if (hidden <= 0 || hidden % 64 != 0)
+    return fail(MCAMD_EUNSUPPORTED, "linear_bf16_gated: hidden must be a multiple of 64");
+  LinParams P;
+  int st = check_linear(x, ldx, w, m, 2 * hidden, k, 1, P);
+  if (st != MCAMD_OK) return st;
+  if (m == 0) {
+    clear_error();
+    return MCAMD_OK;
+  }
+  if (!h || ldh < hidden || ldh % 4 != 0 || !aligned(h, 8))
+    return fail(MCAMD_EINVAL, "linear_bf16_gated: need h with ldh >= hidden (a multiple of 4)");
+  P.y = static_cast<uint16_t *>(h);
+  P.ldy = ldh;
+  P.gated = 1;
+  launch_skinny<8>(P, as_stream(stream));  // a 128-row tile holds 64 gate and their 64 up rows
+  return launch_status("linear_bf16_gated");
 }
 
 extern "C" int mcamd_linear_bf16_partials(const void *x, int64_t ldx, const void *w, float *part,

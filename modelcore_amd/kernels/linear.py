@@ -14,7 +14,8 @@ import torch
 
 from modelcore_amd import _ext
 
-__all__ = ["supported", "linear_bf16", "linear_bf16_partials", "Partials", "k_splits"]
+__all__ = ["supported", "linear_bf16", "linear_bf16_partials", "Partials", "k_splits",
+           "gated_supported", "interleave_gate_up", "linear_bf16_gated"]
 
 MAX_ROWS = 64
 TILE_N = 64     # rows of W per workgroup (four waves)
@@ -116,3 +117,50 @@ def linear_bf16_partials(x: torch.Tensor, w: torch.Tensor, splits: int | None = 
                                                _ext.stream_handle(x.device))
     _ext.check(st, "linear_bf16_partials")
     return Partials(part, s, (*x.shape[:-1], n))
+
+
+GATE_BLOCK = 64  # rows of W_gate, then of W_up, alternating in the interleaved gate/up weight
+
+
+def interleave_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """[W_gate; W_up] with their rows interleaved in blocks of 64 (gate rows 64 b .. 64 b + 63,
+    then the up rows of the same units): the layout linear_bf16_gated reads. (2 hidden, k)."""
+    hid, k = w_gate.shape
+    if w_up.shape != w_gate.shape or hid % GATE_BLOCK:
+        raise ValueError(f"gate {tuple(w_gate.shape)} / up {tuple(w_up.shape)}: need equal shapes "
+                         f"with a multiple of {GATE_BLOCK} rows")
+    return torch.stack([w_gate.reshape(-1, GATE_BLOCK, k), w_up.reshape(-1, GATE_BLOCK, k)],
+                       dim=1).reshape(2 * hid, k)
+
+
+def split_gate_up(out: torch.Tensor):
+    """gate, up (each (..., hidden), strided views) of x . W^T for an interleaved W."""
+    n = out.shape[-1]
+    blocks = out.view(*out.shape[:-1], n // (2 * GATE_BLOCK), 2, GATE_BLOCK)
+    return blocks[..., 0, :], blocks[..., 1, :]
+
+
+def gated_supported(x: torch.Tensor, w: torch.Tensor) -> bool:
+    """Whether linear_bf16_gated(x, w) takes these operands."""
+    return supported(x, w) and w.shape[0] % (2 * GATE_BLOCK) == 0
+
+
+def linear_bf16_gated(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """silu(x . W_gate^T) * (x . W_up^T), (..., hidden) bf16, for the interleaved W of
+    interleave_gate_up; torch's rounding of the separate bf16 ops."""
+    _ext.require_rocm(x, w, what="linear_bf16_gated")
+    if not gated_supported(x, w):
+        raise ValueError(f"linear_bf16_gated takes what linear_bf16 takes, with 2 * 64 | n; got x "
+                         f"{tuple(x.shape)} {x.dtype}, w {tuple(w.shape)} {w.dtype}")
+    n, k = w.shape
+    hid = n // 2
+    x2 = x.reshape(-1, k)
+    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    h = torch.empty(m, hid, dtype=torch.bfloat16, device=x.device)
+    st = _ext.lib().mcamd_linear_bf16_gated(x2.data_ptr(), x2.stride(0), w.data_ptr(),
+                                            h.data_ptr(), hid, m, hid, k, _ext.ACT_SILU,
+                                            _ext.stream_handle(x.device))
+    _ext.check(st, "linear_bf16_gated")
+    return h.view(*x.shape[:-1], hid)

@@ -118,6 +118,7 @@ class Linear(nn.Linear):
     ``Model.cache_inference_weights``, read from a copy cast once (the same values, without the
     per-call cast traffic)."""
     _cast = None
+    _in_stack = False  # its cached rows live only in a stacked copy (gate/up interleaved)
     skinny = False  # set by Model.use_skinny_gemm
     partial = False  # set by Model.set_fused_residual: may return the product's partials
 
@@ -380,12 +381,14 @@ class GatedMLP(nn.Module):
     def __init__(self, n_embd, activation, hidden_dim):
         super().__init__()
         self.n_embd = n_embd
+        self.activation = activation
         self.act = _ACTIVATIONS[activation]
         self.gate_proj = Linear(n_embd, hidden_dim, bias=False)
         self.up_proj = Linear(n_embd, hidden_dim, bias=False)
         self.down_proj = Linear(hidden_dim, n_embd, bias=False)
         self.hidden_dim = hidden_dim
         self._gate_up = None  # [W_gate; W_up] in the compute dtype, set by cache_inference_weights
+        self._gate_up_blocked = False  # rows interleaved in blocks of 64 (linear.interleave_gate_up)
 
     @torch.no_grad()
     def init_weights(self):
@@ -396,6 +399,15 @@ class GatedMLP(nn.Module):
 
     def forward(self, x):
         if self._gate_up is not None and self._gate_up.dtype == x.dtype:
+            if self._gate_up_blocked:
+                from modelcore_amd.kernels import linear as lin
+                if self.gate_proj.skinny and self.activation == "silu" \
+                        and lin.gated_supported(x, self._gate_up):
+                    return self.down_proj(lin.linear_bf16_gated(x, self._gate_up))
+                out = _product(x, self._gate_up, self.gate_proj.skinny)
+                gate, up = lin.split_gate_up(out)
+                return self.down_proj((self.act(gate) * up).reshape(*out.shape[:-1],
+                                                                    self.hidden_dim))
             gate, up = _product(x, self._gate_up, self.gate_proj.skinny).split(self.hidden_dim,
                                                                               dim=-1)
             return self.down_proj(self.act(gate) * up)
@@ -632,21 +644,31 @@ class Model(nn.Module):
                 q, kv = m.c_q.out_features, m.c_k.out_features
                 m.c_q._cast, m.c_k._cast, m.c_v._cast = stacked.split([q, kv, kv])
             elif fuse and isinstance(m, GatedMLP):
-                stacked = torch.cat([m.gate_proj.weight, m.up_proj.weight]).to(dtype)
-                m._gate_up = stacked
-                m.gate_proj._cast, m.up_proj._cast = stacked.split(m.hidden_dim)
+                from modelcore_amd.kernels.linear import GATE_BLOCK, interleave_gate_up
+                if m.hidden_dim % GATE_BLOCK == 0:
+                    # Gate and up rows interleaved in blocks of 64, the layout of the fused
+                    # SiLU-product kernel; the separate gate/up rows have no view of their own.
+                    m._gate_up = interleave_gate_up(m.gate_proj.weight, m.up_proj.weight).to(dtype)
+                    m._gate_up_blocked = True
+                    m.gate_proj._in_stack = m.up_proj._in_stack = True
+                else:
+                    stacked = torch.cat([m.gate_proj.weight, m.up_proj.weight]).to(dtype)
+                    m._gate_up = stacked
+                    m.gate_proj._cast, m.up_proj._cast = stacked.split(m.hidden_dim)
         for m in self.modules():
-            if isinstance(m, Linear) and m._cast is None:
+            if isinstance(m, Linear) and m._cast is None and not m._in_stack:
                 m._cast = m.weight.detach().to(dtype)
 
     def drop_inference_weights(self):
         for m in self.modules():
             if isinstance(m, Linear):
                 m._cast = None
+                m._in_stack = False
             elif isinstance(m, Attention):
                 m._qkv = None
             elif isinstance(m, GatedMLP):
                 m._gate_up = None
+                m._gate_up_blocked = False
 
     def set_fused_residual(self, enabled: bool):
         """Run each block's residual adds and the RMS-norms after them as one launch each

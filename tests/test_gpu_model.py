@@ -225,17 +225,20 @@ def test_skinny_gemm_projections_match_the_library_gemm(monkeypatch):
     mgr = gpu_manager(torch.bfloat16)
     model = awake(mgr.create_model(cfg, device=DEV, seed=0))
     idx = torch.randint(0, cfg.vocab_size, (2, 16), generator=torch.Generator().manual_seed(4)).to(DEV)
-    calls = []
-    real = lin.linear_bf16
+    calls, gated = [], []
+    real, real_gated = lin.linear_bf16, lin.linear_bf16_gated
     monkeypatch.setattr(lin, "linear_bf16", lambda *a, **k: (calls.append(1), real(*a, **k))[1])
+    monkeypatch.setattr(lin, "linear_bf16_gated",
+                        lambda *a, **k: (gated.append(1), real_gated(*a, **k))[1])
     with torch.no_grad():
         model.cache_inference_weights()
         a = model(idx)
-        assert not calls
+        assert not calls and not gated
         model.use_skinny_gemm(True)
         b = model(idx)
         model.use_skinny_gemm(False)
-    assert len(calls) >= 4 * 2  # qkv, c_proj, gate/up, down of both layers (+ lm_head)
+    assert len(calls) >= 3 * 2  # qkv, c_proj, down of both layers (+ lm_head)
+    assert len(gated) == 2  # gate/up with the SiLU product, one per layer
     err = (a.float() - b.float()).abs().max().item()
     print(f"skinny GEMM projections: logits max-abs {err:.4f}", flush=True)
     assert err <= 0.05

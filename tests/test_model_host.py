@@ -240,3 +240,20 @@ def test_prefill_rows_refuses_what_it_cannot_place():
     dst.advance(1)
     with pytest.raises(AssertionError, match="non-empty"):
         dst.prefill_rows(src, [3, 6], 1)
+
+
+def test_interleaved_gate_up_weights_split_back_into_gate_and_up():
+    """interleave_gate_up puts 64 gate rows, then the 64 up rows of the same units, block after
+    block; split_gate_up recovers gate and up of a product with it exactly (CPU)."""
+    from modelcore_amd.kernels.linear import interleave_gate_up, split_gate_up
+    g = torch.Generator().manual_seed(1)
+    wg, wu = torch.randn(192, 32, generator=g), torch.randn(192, 32, generator=g)
+    w = interleave_gate_up(wg, wu)
+    assert torch.equal(w[:64], wg[:64]) and torch.equal(w[64:128], wu[:64])
+    assert torch.equal(w[320:], wu[128:])
+    x = torch.randn(3, 5, 32, generator=g)
+    gate, up = split_gate_up(x @ w.T)
+    torch.testing.assert_close(gate.reshape(3, 5, 192), x @ wg.T, atol=1e-5, rtol=0)
+    torch.testing.assert_close(up.reshape(3, 5, 192), x @ wu.T, atol=1e-5, rtol=0)
+    with pytest.raises(ValueError):
+        interleave_gate_up(wg[:100], wu[:100])
