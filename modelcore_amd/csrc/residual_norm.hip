@@ -9,8 +9,9 @@
 // next block's mixer, or the lm_head) directly.
 //
 // One workgroup of 256 threads per row m; each thread owns chunks of 8 elements (16 bytes of
-// bf16, 32 of fp32 partials), so every load and store is a full 16-byte vector. The mean square
-// is a wave sum (DPP/shuffles) then a sum over the four waves through LDS.
+// bf16, 32 of fp32 partials), so every load and store is a full 16-byte vector, and keeps them in
+// registers between the sum and the norm (rows up to 8192 elements). The mean square is a wave
+// sum (shuffles) then a sum over the four waves through LDS.
 #include "kernels.h"
 
 namespace mcamd {
@@ -45,13 +46,18 @@ __device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
                uint32_t(to_bf16(v[6])) | (uint32_t(to_bf16(v[7])) << 16)};
 }
 
+// CPT > 0: each thread keeps its (at most CPT) chunks of x_out in registers for the norm;
+// CPT = 0: any row length, the norm pass re-reads the thread's own chunks of x_out.
+template <int CPT>
 __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(ResParams P) {
   __shared__ float wsum[kThreads / 64];
   const int m = blockIdx.x;
   const int chunks = P.N / 8;
   const int64_t row = int64_t(m) * P.N;
+  constexpr int kHeld = CPT > 0 ? CPT : 1;
+  float held[kHeld][8];
   float ss = 0.f;
-  for (int c = threadIdx.x; c < chunks; c += kThreads) {
+  auto residual_chunk = [&](int c, float (&sv)[8]) {
     float xv[8], yv[8];
     unpack8(*reinterpret_cast<const uint4 *>(P.x + row + 8 * c), xv);
     if (P.part) {
@@ -68,13 +74,21 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(ResParams P)
     } else {
       unpack8(*reinterpret_cast<const uint4 *>(P.y + row + 8 * c), yv);
     }
-    float sv[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       sv[i] = __uint_as_float(uint32_t(to_bf16(xv[i] + yv[i])) << 16);
       ss = fmaf(sv[i], sv[i], ss);
     }
     *reinterpret_cast<uint4 *>(P.x_out + row + 8 * c) = pack8(sv);
+  };
+  if constexpr (CPT > 0) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int c = threadIdx.x + u * kThreads;
+      if (c < chunks) residual_chunk(c, held[u]);
+    }
+  } else {
+    for (int c = threadIdx.x; c < chunks; c += kThreads) residual_chunk(c, held[0]);
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
@@ -84,13 +98,23 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(ResParams P)
 #pragma unroll
   for (int w = 0; w < kThreads / 64; ++w) total += wsum[w];
   const float r = rsqrtf(total / float(P.N) + P.eps);
-  // Second pass over this thread's own chunks of x_out (its own writes, still in its cache).
-  for (int c = threadIdx.x; c < chunks; c += kThreads) {
-    float sv[8];
-    unpack8(*reinterpret_cast<const uint4 *>(P.x_out + row + 8 * c), sv);
+  auto norm_chunk = [&](int c, float (&sv)[8]) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) sv[i] *= r;
     *reinterpret_cast<uint4 *>(P.h_out + row + 8 * c) = pack8(sv);
+  };
+  if constexpr (CPT > 0) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int c = threadIdx.x + u * kThreads;
+      if (c < chunks) norm_chunk(c, held[u]);
+    }
+  } else {
+    // The thread's own chunks of x_out, written above by this same thread.
+    for (int c = threadIdx.x; c < chunks; c += kThreads) {
+      unpack8(*reinterpret_cast<const uint4 *>(P.x_out + row + 8 * c), held[0]);
+      norm_chunk(c, held[0]);
+    }
   }
 }
 
@@ -127,7 +151,16 @@ extern "C" int mcamd_residual_rmsnorm(const void *x, const float *part, int64_t 
   P.N = int(n);
   P.S = part ? int(splits) : 0;
   P.eps = eps;
-  hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(unsigned(m)), dim3(kThreads), 0,
-                     as_stream(stream), P);
+  const int64_t chunks = n / 8;
+  const dim3 grid{unsigned(m), 1, 1}, block{unsigned(kThreads), 1, 1};
+  hipStream_t s = as_stream(stream);
+  if (chunks <= kThreads)
+    hipLaunchKernelGGL(residual_rmsnorm_kernel<1>, grid, block, 0, s, P);
+  else if (chunks <= 2 * kThreads)
+    hipLaunchKernelGGL(residual_rmsnorm_kernel<2>, grid, block, 0, s, P);
+  else if (chunks <= 4 * kThreads)
+    hipLaunchKernelGGL(residual_rmsnorm_kernel<4>, grid, block, 0, s, P);
+  else
+    hipLaunchKernelGGL(residual_rmsnorm_kernel<0>, grid, block, 0, s, P);
   return launch_status("residual_rmsnorm");
 }

@@ -45,7 +45,8 @@ def _check(got, want):
     assert torch.all(err <= wh.abs() * 2.0 ** -8 + 1e-6), float(err.max())
 
 
-@pytest.mark.parametrize("m,n,splits", [(1, 4096, 1), (7, 384, 2), (64, 4096, 4), (33, 8, 3)])
+@pytest.mark.parametrize("m,n,splits", [(1, 4096, 1), (7, 384, 2), (64, 4096, 4), (33, 8, 3),
+                                          (3, 14336, 2), (2, 8200, 1)])
 def test_partials_are_summed_added_and_normed(m, n, splits):
     _note("residual partials", m, n, splits)
     g = torch.Generator().manual_seed(m * 7 + n + splits)
