@@ -165,6 +165,23 @@ int mcamd_qk_rope_norm_append(const void *q, int64_t q_token_stride, const void 
                               int dtype, void *stream);
 
 /*
+ * mcamd_qk_rope_norm_append for bf16, reading q, k, v from the unsummed K-split partials of the
+ * stacked QKV projection (mcamd_linear_bf16_partials of x with [W_q; W_k; W_v]): `part` is
+ * (splits, batch * t_new, part_token_stride) fp32, q at columns [0, H D), k at [H D, (H + H_kv) D),
+ * v after it; each value is the in-order sum of the splits rounded to bf16, which is what
+ * mcamd_linear_bf16 outputs. with_kv = 0: q only (k_cache, v_cache unused). Saves the projection's
+ * separate reduce pass; otherwise as mcamd_qk_rope_norm_append.
+ */
+int mcamd_qk_rope_norm_append_partials(const float *part, int64_t splits,
+                                       int64_t part_token_stride, const void *cos,
+                                       const void *sin, int64_t n_pos, void *k_cache,
+                                       void *v_cache, const int32_t *cache_seqlens, void *q_out,
+                                       int64_t batch, int64_t t_new, int64_t n_head,
+                                       int64_t n_kv_head, int64_t head_dim, int64_t t_max,
+                                       int64_t cache_batch_stride, float eps, float scale,
+                                       int with_kv, void *stream);
+
+/*
  * y = x . W^T for decode-sized batches: x (m, k) bf16 rows `ldx` elements apart, m <= 64; W
  * (n, k) bf16 contiguous (the nn.Linear weight layout); y (m, n) bf16 rows `ldy` apart; fp32
  * accumulation. n must be a multiple of 64 and k of 128 * k_splits. With k_splits > 1 the K

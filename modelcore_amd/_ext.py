@@ -51,6 +51,10 @@ SIGNATURES = {
                                          _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64,
                                          _i64, _i64, ctypes.c_float, ctypes.c_float, _int,
                                          _ptr]),
+    "mcamd_qk_rope_norm_append_partials": (_int, [_ptr, _i64, _i64, _ptr, _ptr, _i64, _ptr, _ptr,
+                                                  _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64,
+                                                  _i64, ctypes.c_float, ctypes.c_float, _int,
+                                                  _ptr]),
     "mcamd_linear_bf16_workspace_bytes": (_size, [_i64, _i64, _i64]),
     "mcamd_linear_bf16": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr,
                                  _size, _ptr]),

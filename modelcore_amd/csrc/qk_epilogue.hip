@@ -71,6 +71,12 @@ struct EpiParams {
   int64_t q_tok, k_tok, v_tok;  // elements between consecutive tokens of q, k, v
   int t_new, H, H_kv, D, n_items;
   float eps, scale;
+  // Or, instead of q, k, v: the unsummed K-split partials of the stacked QKV projection,
+  // (part_S, n_tokens, part_tok) fp32, q / k / v at columns 0, H D, (H + H_kv) D of a row; each
+  // value is their in-order sum rounded to bf16, as the GEMM's own reduce pass makes it.
+  const float *part;
+  int64_t part_tok, part_slice;
+  int part_S;
 };
 
 template <bool BF16>
@@ -91,18 +97,32 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void qk_epilogue_kernel(EpiPar
   const bool in_table = pos >= 0 && pos < P.n_pos;
   const bool in_cache = pos >= 0 && pos < P.t_max;
 
-  // Item order: H query heads, then H_kv key heads, then H_kv value heads.
+  // Element j of this item's source row, from q/k/v or from the projection's partials (whose
+  // columns follow the item order: H query heads, then H_kv key heads, then H_kv value heads).
+  const float *psrc = P.part ? P.part + tok * P.part_tok + int64_t(item) * P.D : nullptr;
+  auto part_load = [&](int j) {
+    float a = 0.f;
+    for (int s = 0; s < P.part_S; ++s) a += psrc[int64_t(s) * P.part_slice + j];
+    return round_bf16(a);
+  };
+
   if (item >= P.H + P.H_kv) {  // v: plain copy into the cache
     if (!in_cache) return;
     const int hk = item - P.H - P.H_kv;
-    const T *src = static_cast<const T *>(P.v) + tok * P.v_tok + int64_t(hk) * P.D;
     T *dst = static_cast<T *>(P.v_cache) + int64_t(b) * P.cache_b + (pos * P.H_kv + hk) * P.D;
+    if (psrc) {
+      for (int d = lane; d < P.D; d += 64) E::store(dst + d, part_load(d));
+      return;
+    }
+    const T *src = static_cast<const T *>(P.v) + tok * P.v_tok + int64_t(hk) * P.D;
     for (int d = lane; d < P.D; d += 64) dst[d] = src[d];
     return;
   }
   const bool is_q = item < P.H;
-  const T *src = is_q ? static_cast<const T *>(P.q) + tok * P.q_tok + int64_t(item) * P.D
-                      : static_cast<const T *>(P.k) + tok * P.k_tok + int64_t(item - P.H) * P.D;
+  const T *src = psrc ? nullptr
+                 : is_q ? static_cast<const T *>(P.q) + tok * P.q_tok + int64_t(item) * P.D
+                        : static_cast<const T *>(P.k) + tok * P.k_tok + int64_t(item - P.H) * P.D;
+  auto load = [&](int j) { return psrc ? part_load(j) : E::load(src + j); };
   T *dst;
   if (is_q) {
     dst = static_cast<T *>(P.q_out) + (tok * P.H + item) * P.D;
@@ -124,7 +144,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void qk_epilogue_kernel(EpiPar
   for (int r = 0; r < 2; ++r) {
     const int j = lane + 64 * r;
     if (j < half) {
-      const float x1 = E::load(src + j), x2 = E::load(src + j + half);
+      const float x1 = load(j), x2 = load(j + half);
       const float c = E::load(cs + j), s = E::load(sn + j);
       y1[r] = E::rnd(E::rnd(x1 * c) + E::rnd(x2 * s));
       y2[r] = E::rnd(E::rnd(x1 * -s) + E::rnd(x2 * c));
@@ -183,7 +203,7 @@ extern "C" int mcamd_qk_rope_norm_append(const void *q, int64_t q_token_stride, 
   if (q_token_stride < n_head * head_dim ||
       (with_kv && (k_token_stride < n_kv_head * head_dim || v_token_stride < n_kv_head * head_dim)))
     return fail(MCAMD_EINVAL, "qk_rope_norm_append: a token stride is smaller than heads * head_dim");
-  EpiParams P;
+  EpiParams P{};
   P.q = q;
   P.k = k;
   P.v = v;
@@ -219,4 +239,64 @@ extern "C" int mcamd_qk_rope_norm_append(const void *q, int64_t q_token_stride, 
     hipLaunchKernelGGL(qk_epilogue_kernel<false>, dim3(unsigned(blocks)),
                        dim3(64 * kWavesPerBlock), 0, as_stream(stream), P);
   return launch_status("qk_rope_norm_append");
+}
+
+extern "C" int mcamd_qk_rope_norm_append_partials(
+    const float *part, int64_t splits, int64_t part_token_stride, const void *cos,
+    const void *sin, int64_t n_pos, void *k_cache, void *v_cache, const int32_t *cache_seqlens,
+    void *q_out, int64_t batch, int64_t t_new, int64_t n_head, int64_t n_kv_head,
+    int64_t head_dim, int64_t t_max, int64_t cache_batch_stride, float eps, float scale,
+    int with_kv, void *stream) {
+  if (batch < 0 || t_new < 0 || n_head <= 0 || n_kv_head <= 0 || n_pos <= 0)
+    return fail(MCAMD_EINVAL, "qk_rope_norm_append_partials: sizes must be positive");
+  if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > 256)
+    return fail(MCAMD_EUNSUPPORTED, "qk_rope_norm_append_partials: head_dim must be even, <= 256");
+  if (splits < 1 || splits > 64)
+    return fail(MCAMD_EINVAL, "qk_rope_norm_append_partials: splits must be in [1, 64]");
+  if (!(eps >= 0.f) || !std::isfinite(scale))
+    return fail(MCAMD_EINVAL, "qk_rope_norm_append_partials: eps must be >= 0 and scale finite");
+  const int64_t width = (n_head + (with_kv ? 2 * n_kv_head : 0)) * head_dim;
+  if (part_token_stride < width)
+    return fail(MCAMD_EINVAL, "qk_rope_norm_append_partials: token stride smaller than the row");
+  if (batch * t_new == 0) {
+    clear_error();
+    return MCAMD_OK;
+  }
+  if (!part || !cos || !sin || !cache_seqlens || !q_out ||
+      (with_kv && (!k_cache || !v_cache || t_max <= 0)))
+    return fail(MCAMD_EINVAL, "qk_rope_norm_append_partials: null pointer or empty cache");
+  if (with_kv && cache_batch_stride < t_max * n_kv_head * head_dim)
+    return fail(MCAMD_EINVAL,
+                "qk_rope_norm_append_partials: cache_batch_stride smaller than T_max*H_kv*D");
+  if (t_new > 0x7fffffff || n_head + 2 * n_kv_head > 0x7fffffff)
+    return fail(MCAMD_EUNSUPPORTED, "qk_rope_norm_append_partials: sizes too large");
+  EpiParams P{};
+  P.part = part;
+  P.part_S = int(splits);
+  P.part_tok = part_token_stride;
+  P.part_slice = batch * t_new * part_token_stride;
+  P.cos = cos;
+  P.sin = sin;
+  P.k_cache = k_cache;
+  P.v_cache = v_cache;
+  P.q_out = q_out;
+  P.seqlens = cache_seqlens;
+  P.n_tokens = batch * t_new;
+  P.n_pos = n_pos;
+  P.t_max = with_kv ? t_max : 0;
+  P.cache_b = cache_batch_stride;
+  P.t_new = int(t_new);
+  P.H = int(n_head);
+  P.H_kv = int(n_kv_head);
+  P.D = int(head_dim);
+  P.n_items = int(n_head + (with_kv ? 2 * n_kv_head : 0));
+  P.eps = eps;
+  P.scale = scale;
+  const int64_t waves = P.n_tokens * P.n_items;
+  const int64_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
+  if (blocks > 0x7fffffff)
+    return fail(MCAMD_EUNSUPPORTED, "qk_rope_norm_append_partials: grid too large");
+  hipLaunchKernelGGL(qk_epilogue_kernel<true>, dim3(unsigned(blocks)), dim3(64 * kWavesPerBlock),
+                     0, as_stream(stream), P);
+  return launch_status("qk_rope_norm_append_partials");
 }

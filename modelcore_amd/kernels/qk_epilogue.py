@@ -25,7 +25,7 @@ import torch
 
 from modelcore_amd import _ext
 
-__all__ = ["rope_norm_scale_append", "default_eps"]
+__all__ = ["rope_norm_scale_append", "rope_norm_scale_append_partials", "default_eps"]
 
 
 def default_eps() -> float:
@@ -126,4 +126,51 @@ def rope_norm_scale_append(q, cos, sin, cache_seqlens, k=None, v=None, k_cache=N
         v_cache.data_ptr() if k is not None else None, seqlens.data_ptr(), out.data_ptr(), B, T,
         H, H_kv, D, T_max, cb, eps, float(scale), code, _ext.stream_handle(q.device))
     _ext.check(st, "rope_norm_scale_append")
+    return out
+
+
+def rope_norm_scale_append_partials(qkv, n_head, n_kv_head, cos, sin, cache_seqlens,
+                                    k_cache=None, v_cache=None, eps=None, scale=1.2):
+    """rope_norm_scale_append for bf16, with q, k, v taken from the unsummed K-split partials of
+    the stacked QKV projection (``qkv``: a ``linear.Partials`` of shape (B, T, (H + 2 H_kv) D),
+    or (B, T, H D) with no caches: q only). Each value is the in-order sum of the partials rounded
+    to bf16 -- the projection's own output -- so the result is that of rope_norm_scale_append on
+    the summed projection, without its separate reduce pass. Returns q (B, T, H, D) bf16."""
+    from modelcore_amd.kernels.linear import Partials
+    if not isinstance(qkv, Partials):
+        raise TypeError("qkv must be the Partials of the stacked QKV projection")
+    part = qkv.part
+    _ext.require_rocm(part, k_cache, v_cache, cache_seqlens, what="rope_norm_scale_append_partials")
+    B, T, n = qkv.shape
+    with_kv = k_cache is not None
+    D = n // (n_head + (2 * n_kv_head if with_kv else 0))
+    if D * (n_head + (2 * n_kv_head if with_kv else 0)) != n or D % 2:
+        raise ValueError(f"a row of {n} is not (H + 2 H_kv) * D with even D for H={n_head}, "
+                         f"H_kv={n_kv_head}")
+    if part.dtype != torch.float32 or part.shape != (qkv.splits, B * T, n) \
+            or not part.is_contiguous():
+        raise ValueError("partials must be contiguous (splits, B*T, n) fp32")
+    half = D // 2
+    dt = torch.bfloat16
+    cos_t, sin_t = _table(cos, half, dt, part.device), _table(sin, half, dt, part.device)
+    if cache_seqlens.dtype != torch.int32 or cache_seqlens.shape != (B,):
+        raise ValueError(f"cache_seqlens must be ({B},) int32")
+    T_max, cb = 0, 0
+    if with_kv:
+        if k_cache.shape != v_cache.shape or k_cache.dim() != 4 or k_cache.shape[0] != B \
+                or k_cache.shape[2:] != (n_kv_head, D) or k_cache.dtype != dt \
+                or v_cache.dtype != dt:
+            raise ValueError(f"k_cache/v_cache must be (B, T_max, H_kv, D) = ({B}, T_max, "
+                             f"{n_kv_head}, {D}) bf16")
+        if k_cache.stride() != v_cache.stride() or not k_cache[0].is_contiguous():
+            raise ValueError("each row of k_cache/v_cache must be contiguous, with equal strides")
+        T_max, cb = k_cache.shape[1], k_cache.stride(0)
+    out = torch.empty((B, T, n_head, D), dtype=dt, device=part.device)
+    st = _ext.lib().mcamd_qk_rope_norm_append_partials(
+        part.data_ptr(), qkv.splits, n, cos_t.data_ptr(), sin_t.data_ptr(), cos_t.shape[0],
+        k_cache.data_ptr() if with_kv else None, v_cache.data_ptr() if with_kv else None,
+        cache_seqlens.contiguous().data_ptr(), out.data_ptr(), B, T, n_head, n_kv_head, D, T_max,
+        cb, default_eps() if eps is None else float(eps), float(scale), int(with_kv),
+        _ext.stream_handle(part.device))
+    _ext.check(st, "rope_norm_scale_append_partials")
     return out

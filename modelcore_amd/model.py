@@ -322,11 +322,28 @@ class Attention(nn.Module):
         return (q, self.c_k(x).view(B, T, self.n_kv_head, D),
                 self.c_v(x).view(B, T, self.n_kv_head, D))
 
+    qkv_partial = False  # set by Model.set_fused_residual
+
+    def _qkv_partials(self, x):
+        """The stacked QKV product as unsummed K-split partials, when the fused pre-attention
+        step can sum them itself (the native epilogue, bf16, decode-sized rows), else None."""
+        if not (self.qkv_partial and self.produces_kv and self._qkv is not None
+                and self._qkv.dtype == x.dtype and self.c_q.skinny
+                and self.epilogue is _default_epilogue()):
+            return None
+        from modelcore_amd.kernels import linear as lin
+        return lin.linear_bf16_partials(x, self._qkv) if lin.supported(x, self._qkv) else None
+
     def forward(self, x, kv_cache, kv_bus):
         B, T, _ = x.size()
+        fused = kv_cache is not None and self.epilogue is not None and self.fuse_epilogue \
+            and isinstance(self.norm, RMSNorm)
+        if fused:
+            part = self._qkv_partials(x)
+            if part is not None:
+                return self._forward_fused(x, None, None, None, kv_cache, kv_bus, part)
         q, k, v = self._project(x)
-        if kv_cache is not None and self.epilogue is not None and self.fuse_epilogue \
-                and isinstance(self.norm, RMSNorm):
+        if fused:
             return self._forward_fused(x, q, k, v, kv_cache, kv_bus)
         if self.produces_kv:
             q, k = self.rope(q, k, kv_cache)
@@ -348,7 +365,7 @@ class Attention(nn.Module):
             y = self.features["output_gate"](y, x)
         return self.c_proj(y.contiguous().view(B, T, -1))
 
-    def _forward_fused(self, x, q, k, v, kv_cache, kv_bus):
+    def _forward_fused(self, x, q, k, v, kv_cache, kv_bus, qkv_part=None):
         """The same layer with the pre-attention ops fused: a producer rotates, norms and scales
         q and k and appends k, v to its slot in one launch; a KV-sharing consumer finds them there
         already (the reference's consumer re-appends identical values, attention.py:70-80), so it
@@ -357,7 +374,13 @@ class Attention(nn.Module):
         self.rope.check_positions(T, kv_cache)
         k_cache, v_cache = kv_cache.get_slot_cache(self.kv_slot)
         seqlens = kv_cache.cache_seqlens
-        if self.produces_kv:
+        if qkv_part is not None:
+            from modelcore_amd.kernels.qk_epilogue import rope_norm_scale_append_partials
+            q = rope_norm_scale_append_partials(qkv_part, self.n_head, self.n_kv_head,
+                                                self.rope.cos, self.rope.sin, seqlens, k_cache,
+                                                v_cache, eps=self.norm.eps, scale=1.2)
+            kv_bus[self.kv_slot] = None
+        elif self.produces_kv:
             q = self.epilogue(q, self.rope.cos, self.rope.sin, seqlens, k, v, k_cache, v_cache,
                               eps=self.norm.eps, scale=1.2)
             kv_bus[self.kv_slot] = None  # consumers read the slot itself
@@ -674,12 +697,14 @@ class Model(nn.Module):
         """Run each block's residual adds and the RMS-norms after them as one launch each
         (residual_rmsnorm), with the norm carried into the next block and the lm_head, and let
         c_proj / down_proj hand over their unsummed K-split partials when they run on the skinny
-        GEMM. For bf16 decode-sized rows; results differ from the separate ops only in the order
+        GEMM (and the stacked QKV product its partials to the fused pre-attention step, which
+        sums them). For bf16 decode-sized rows; results differ from the separate ops only in the order
         of the norm's fp32 sum of squares. Needs the parameterless RMSNorm."""
         if enabled and not isinstance(self.shared["norm"], RMSNorm):
             raise NotImplementedError("fused residual steps need the rms_norm shared norm")
         for block in self.body.blocks:
             block.fuse_residual = bool(enabled)
+            block.mixer.qkv_partial = bool(enabled)
             block.mixer.c_proj.partial = bool(enabled)
             out = getattr(block.ffn, "down_proj", None) or block.ffn.c_proj
             out.partial = bool(enabled)

@@ -154,3 +154,36 @@ def test_the_step_is_stream_ordered_and_syncs_nothing():
         assert torch.equal(out, eager), i
         assert torch.equal(kc[:, 9], ref_k[:, 9]), i
     assert _ext.lib() is not None
+
+
+@pytest.mark.parametrize("with_kv", [True, False], ids=["producer", "q-only"])
+def test_partials_of_the_qkv_projection_give_the_summed_projection_result(with_kv):
+    """The epilogue fed the unsummed K-split partials of the stacked QKV product equals, bit for
+    bit, the epilogue fed that product's bf16 output (q, caches); the partials' in-order sum
+    rounded to bf16 is exactly what the GEMM outputs."""
+    from modelcore_amd.kernels.linear import linear_bf16, linear_bf16_partials
+    from modelcore_amd.kernels.qk_epilogue import rope_norm_scale_append_partials
+    _note("epilogue from qkv partials", with_kv)
+    B, H, H_kv, D, T_max, K = 5, 8, 2, 128, 40, 1024
+    g = torch.Generator().manual_seed(12)
+    n = (H + (2 * H_kv if with_kv else 0)) * D
+    x = torch.randn(B, 1, K, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(n, K, generator=g) * K ** -0.5).to(torch.bfloat16).to(DEV)
+    cos, sin = (t.to(DEV) for t in rope_tables(64, D, "cpu", torch.bfloat16))
+    seqlens = torch.tensor([0, 3, 17, 30, 38], dtype=torch.int32, device=DEV)
+    kc = torch.randn(B, T_max, H_kv, D, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(B, T_max, H_kv, D, generator=g).to(torch.bfloat16).to(DEV)
+    kc2, vc2 = kc.clone(), vc.clone()
+    part = linear_bf16_partials(x, w, splits=4)
+    got = rope_norm_scale_append_partials(part, H, H_kv, cos, sin, seqlens,
+                                          kc if with_kv else None, vc if with_kv else None)
+    y = linear_bf16(x, w, 4)
+    q = y[..., :H * D].view(B, 1, H, D)
+    if with_kv:
+        k = y[..., H * D:(H + H_kv) * D].view(B, 1, H_kv, D)
+        v = y[..., (H + H_kv) * D:].view(B, 1, H_kv, D)
+        want = rope_norm_scale_append(q, cos, sin, seqlens, k, v, kc2, vc2)
+    else:
+        want = rope_norm_scale_append(q, cos, sin, seqlens)
+    assert torch.equal(got, want)
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
