@@ -3,10 +3,13 @@ activations, the projection GEMMs of a decode step (``F.linear`` in the referenc
 ``Linear.forward``, modelcore/components/linear.py:13-14).
 
 With 64 or fewer rows each weight byte is used at most 64 times, so the product is bound by
-reading W once from HBM. ``mcamd_linear_bf16`` streams 64-row tiles of W (and the activations)
-through LDS with coalesced loads; when N has too few tiles to fill the GPU the K range is split
-and the partial products are summed in a fixed order by a second kernel (deterministic, fp32
-accumulation). ``supported`` says which shapes it takes.
+reading W once from HBM. ``mcamd_linear_bf16`` streams tiles of W (128 rows for wide products,
+64 otherwise) and the activations through LDS with coalesced loads; when N has too few tiles to
+fill the GPU the K range is split and the partial products are summed in a fixed order by a
+second kernel (deterministic, fp32 accumulation). ``linear_bf16_partials`` leaves that sum to a
+consumer that sums them itself (the fused residual and pre-attention steps), and
+``linear_bf16_gated`` computes a gated MLP's ``silu(x W_gate^T) * (x W_up^T)`` from W_gate and
+W_up interleaved in 64-row blocks. ``supported`` says which shapes they take.
 """
 from __future__ import annotations
 
@@ -31,7 +34,7 @@ def supported(x: torch.Tensor, w: torch.Tensor) -> bool:
             or w.device != x.device or w.dim() != 2 or not w.is_contiguous():
         return False
     n, k = w.shape
-    if x.shape[-1] != k or n % TILE_N or k % STAGE_K or TILE_N * k * 2 >= 2 ** 31:
+    if x.shape[-1] != k or n % TILE_N or k % STAGE_K or 128 * k * 2 >= 2 ** 31:
         return False
     rows = x.numel() // k if k else 0
     return 0 < rows <= MAX_ROWS
