@@ -411,7 +411,7 @@ class GatedMLP(nn.Module):
         self.down_proj = Linear(hidden_dim, n_embd, bias=False)
         self.hidden_dim = hidden_dim
         self._gate_up = None  # [W_gate; W_up] in the compute dtype, set by cache_inference_weights
-        self._gate_up_blocked = False  # rows interleaved in blocks of 64 (linear.interleave_gate_up)
+        self._gate_up_blocked = False  # rows in 64-row blocks (linear.interleave_gate_up)
 
     @torch.no_grad()
     def init_weights(self):
@@ -698,8 +698,8 @@ class Model(nn.Module):
         (residual_rmsnorm), with the norm carried into the next block and the lm_head, and let
         c_proj / down_proj hand over their unsummed K-split partials when they run on the skinny
         GEMM (and the stacked QKV product its partials to the fused pre-attention step, which
-        sums them). For bf16 decode-sized rows; results differ from the separate ops only in the order
-        of the norm's fp32 sum of squares. Needs the parameterless RMSNorm."""
+        sums them). For bf16 decode-sized rows; results differ from the separate ops only in the
+        order of the norm's fp32 sum of squares. Needs the parameterless RMSNorm."""
         if enabled and not isinstance(self.shared["norm"], RMSNorm):
             raise NotImplementedError("fused residual steps need the rms_norm shared norm")
         for block in self.body.blocks:
