@@ -201,13 +201,16 @@ int mcamd_linear_bf16(const void *x, int64_t ldx, const void *w, void *y, int64_
  * same units; W is (2 hidden, k)), writes h (m, hidden) bf16, rows `ldh` apart:
  *   h[r][j] = bf16(bf16(act(g)) * u),  g = bf16(x[r] . W_gate[j]),  u = bf16(x[r] . W_up[j])
  * in fp32 arithmetic, i.e. torch's `act(gate(x)) * up(x)` on bf16 tensors. act = MCAMD_ACT_SILU
- * (x / (1 + e^-x)); hidden a multiple of 64, k of 128, m <= 64. Replaces GatedMLP.forward's
- * gate_proj, up_proj and the activation product (modelcore/components/mlp.py:89-90) before
- * down_proj.
+ * (x / (1 + e^-x)); hidden a multiple of 64, k of 128, m <= 64. w_tiled = 1: W is stored as
+ * (2 hidden / 64, k / 128, 64, 128) contiguous blocks (block [g][s] = rows 64 g .. 64 g + 63,
+ * columns 128 s .. 128 s + 127, row-major), so that the weight stream reads whole 1 KB runs;
+ * 0: row-major (2 hidden, k). Replaces GatedMLP.forward's gate_proj, up_proj and the activation
+ * product (modelcore/components/mlp.py:89-90) before down_proj.
  */
 enum { MCAMD_ACT_SILU = 0 };
 int mcamd_linear_bf16_gated(const void *x, int64_t ldx, const void *w, void *h, int64_t ldh,
-                            int64_t m, int64_t hidden, int64_t k, int act, void *stream);
+                            int64_t m, int64_t hidden, int64_t k, int act, int w_tiled,
+                            void *stream);
 
 /*
  * mcamd_linear_bf16 without the sum: the K-split partial products, written to `part` as

@@ -22,7 +22,7 @@ LIB_PATH = Path(os.environ.get("MODELCORE_AMD_LIB",
 F32, BF16 = 0, 1
 ACT_SILU = 0  # mcamd_linear_bf16_gated activations
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH = 0, -1, -2, -3, -4
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -59,7 +59,7 @@ SIGNATURES = {
     "mcamd_linear_bf16": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr,
                                  _size, _ptr]),
     "mcamd_linear_bf16_gated": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _int,
-                                       _ptr]),
+                                       _int, _ptr]),
     "mcamd_linear_bf16_partials": (_int, [_ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr]),
     "mcamd_residual_rmsnorm": (_int, [_ptr, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64,
                                       ctypes.c_float, _ptr]),

@@ -47,7 +47,7 @@ int check_attn_shapes(const AttnArgs &a, bool need_workspace) {
 
 using namespace mcamd;
 
-extern "C" int mcamd_abi_version(void) { return 3; }
+extern "C" int mcamd_abi_version(void) { return 4; }
 
 extern "C" const char *mcamd_last_error(void) { return g_last_error.c_str(); }
 

@@ -49,6 +49,7 @@ struct LinParams {
   int M, N, K, S;
   int raw;      // write the partials (fp32) even for S = 1, and leave the sum to the consumer
   int gated;    // W holds [gate; up] interleaved in 64-row blocks: write silu(gate) * up to y
+  int w_tiled;  // W stored as (N / 64, K / 128, 64, 128) blocks instead of row-major (N, K)
 };
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
@@ -137,9 +138,15 @@ __global__ __launch_bounds__(64 * WAVES, 1) void linear_skinny_kernel(LinParams 
       const int r0 = 4 * (4 * wave + jj);
       const int r = r0 + drow;
       const uint32_t chunk = uint32_t(dslot ^ (r & 15));
+      // Row-major: row r of the tile, bytes kb .. kb + 255. Tiled: the tile's 64-row group
+      // r / 64 (K * 128 bytes each, at the same place as in row-major), its 16 KB block of this
+      // stage, row r % 64 of the block -- an instruction reads 1 KB contiguous.
+      const uint32_t wo = P.w_tiled ? uint32_t(r >> 6) * uint32_t(P.K) * 128u + kb * 64u +
+                                          uint32_t(r & 63) * 256u + chunk * 16u
+                                    : uint32_t(r) * uint32_t(P.K) * 2u + kb + chunk * 16u;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rw, (__attribute__((address_space(3))) void *)(&sW[buf][r0 * KC]), 16,
-          int(uint32_t(r) * uint32_t(P.K) * 2u + kb + chunk * 16u), 0, 0, kNonTemporal);
+          rw, (__attribute__((address_space(3))) void *)(&sW[buf][r0 * KC]), 16, int(wo), 0, 0,
+          kNonTemporal);
     }
 #pragma unroll
     for (int u = 0; u < kXPer; ++u) {
@@ -378,7 +385,7 @@ extern "C" int mcamd_linear_bf16(const void *x, int64_t ldx, const void *w, void
 
 extern "C" int mcamd_linear_bf16_gated(const void *x, int64_t ldx, const void *w, void *h,
                                        int64_t ldh, int64_t m, int64_t hidden, int64_t k, int act,
-                                       void *stream) {
+                                       int w_tiled, void *stream) {
   if (act != MCAMD_ACT_SILU)
     return fail(MCAMD_EUNSUPPORTED, "linear_bf16_gated: only silu is supported");
   if (hidden <= 0 || hidden % 64 != 0)
@@ -395,6 +402,7 @@ extern "C" int mcamd_linear_bf16_gated(const void *x, int64_t ldx, const void *w
   P.y = static_cast<uint16_t *>(h);
   P.ldy = ldh;
   P.gated = 1;
+  P.w_tiled = w_tiled != 0;
   launch_skinny<8>(P, as_stream(stream));  // a 128-row tile holds 64 gate and their 64 up rows
   return launch_status("linear_bf16_gated");
 }

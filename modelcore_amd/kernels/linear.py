@@ -18,7 +18,8 @@ import torch
 from modelcore_amd import _ext
 
 __all__ = ["supported", "linear_bf16", "linear_bf16_partials", "Partials", "k_splits",
-           "gated_supported", "interleave_gate_up", "linear_bf16_gated"]
+           "gated_supported", "interleave_gate_up", "linear_bf16_gated", "tile_weight",
+           "untile_weight"]
 
 MAX_ROWS = 64
 TILE_N = 64     # rows of W per workgroup (four waves)
@@ -143,19 +144,50 @@ def split_gate_up(out: torch.Tensor):
     return blocks[..., 0, :], blocks[..., 1, :]
 
 
+TILE_ROWS, TILE_K = 64, 128  # one block of a tiled weight: 64 rows x 128 columns, 16 KB
+
+
+def tile_weight(w: torch.Tensor) -> torch.Tensor:
+    """(n, k) -> (n / 64, k / 128, 64, 128) contiguous blocks: the layout in which the weight
+    stream of the gated product reads whole 1 KB runs (a copy; untile_weight undoes it)."""
+    n, k = w.shape
+    if n % TILE_ROWS or k % TILE_K:
+        raise ValueError(f"tiling needs n % {TILE_ROWS} == 0 and k % {TILE_K} == 0; got "
+                         f"{tuple(w.shape)}")
+    return w.reshape(n // TILE_ROWS, TILE_ROWS, k // TILE_K, TILE_K).transpose(1, 2).contiguous()
+
+
+def untile_weight(wt: torch.Tensor) -> torch.Tensor:
+    """The row-major (n, k) weight of a tile_weight result (a copy)."""
+    g, s, r, c = wt.shape
+    return wt.transpose(1, 2).reshape(g * r, s * c)
+
+
 def gated_supported(x: torch.Tensor, w: torch.Tensor) -> bool:
-    """Whether linear_bf16_gated(x, w) takes these operands."""
-    return supported(x, w) and w.shape[0] % (2 * GATE_BLOCK) == 0
+    """Whether linear_bf16_gated(x, w) takes these operands (w row-major or tiled)."""
+    if w.dim() != 4:
+        return supported(x, w) and w.shape[0] % (2 * GATE_BLOCK) == 0
+    if w.shape[2:] != (TILE_ROWS, TILE_K) or not w.is_contiguous():
+        return False
+    n, k = w.shape[0] * TILE_ROWS, w.shape[1] * TILE_K
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or x.device.type != "cuda" \
+            or w.device != x.device:
+        return False
+    if x.shape[-1] != k or n % (2 * GATE_BLOCK) or 128 * k * 2 >= 2 ** 31:
+        return False
+    return 0 < x.numel() // k <= MAX_ROWS
 
 
 def linear_bf16_gated(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """silu(x . W_gate^T) * (x . W_up^T), (..., hidden) bf16, for the interleaved W of
-    interleave_gate_up; torch's rounding of the separate bf16 ops."""
+    interleave_gate_up, row-major or tiled (tile_weight); torch's rounding of the separate bf16
+    ops."""
     _ext.require_rocm(x, w, what="linear_bf16_gated")
     if not gated_supported(x, w):
         raise ValueError(f"linear_bf16_gated takes what linear_bf16 takes, with 2 * 64 | n; got x "
                          f"{tuple(x.shape)} {x.dtype}, w {tuple(w.shape)} {w.dtype}")
-    n, k = w.shape
+    tiled = w.dim() == 4
+    n, k = (w.shape[0] * TILE_ROWS, w.shape[1] * TILE_K) if tiled else w.shape
     hid = n // 2
     x2 = x.reshape(-1, k)
     if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
@@ -164,6 +196,6 @@ def linear_bf16_gated(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     h = torch.empty(m, hid, dtype=torch.bfloat16, device=x.device)
     st = _ext.lib().mcamd_linear_bf16_gated(x2.data_ptr(), x2.stride(0), w.data_ptr(),
                                             h.data_ptr(), hid, m, hid, k, _ext.ACT_SILU,
-                                            _ext.stream_handle(x.device))
+                                            int(tiled), _ext.stream_handle(x.device))
     _ext.check(st, "linear_bf16_gated")
     return h.view(*x.shape[:-1], hid)

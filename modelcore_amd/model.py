@@ -427,7 +427,8 @@ class GatedMLP(nn.Module):
                 if self.gate_proj.skinny and self.activation == "silu" \
                         and lin.gated_supported(x, self._gate_up):
                     return self.down_proj(lin.linear_bf16_gated(x, self._gate_up))
-                out = _product(x, self._gate_up, self.gate_proj.skinny)
+                w = self._gate_up if self._gate_up.dim() == 2 else lin.untile_weight(self._gate_up)
+                out = _product(x, w, self.gate_proj.skinny)
                 gate, up = lin.split_gate_up(out)
                 return self.down_proj((self.act(gate) * up).reshape(*out.shape[:-1],
                                                                     self.hidden_dim))
@@ -681,6 +682,8 @@ class Model(nn.Module):
         for m in self.modules():
             if isinstance(m, Linear) and m._cast is None and not m._in_stack:
                 m._cast = m.weight.detach().to(dtype)
+        if any(isinstance(m, Linear) and m.skinny for m in self.modules()):
+            self.use_skinny_gemm(True)  # the stacks' layout for the skinny GEMM
 
     def drop_inference_weights(self):
         for m in self.modules():
@@ -711,10 +714,20 @@ class Model(nn.Module):
 
     def use_skinny_gemm(self, enabled: bool):
         """Run the projections of decode-sized batches (at most 64 rows, bf16 cached weights)
-        through ``mcamd_linear_bf16`` instead of F.linear; other shapes keep F.linear."""
+        through ``mcamd_linear_bf16`` instead of F.linear; other shapes keep F.linear. The
+        interleaved gate/up stacks are kept tiled while it is on (``linear.tile_weight``: the
+        gated product then streams whole 1 KB runs of them), row-major while it is off; a library
+        product on a tiled stack (a prefill) reads a row-major copy."""
+        from modelcore_amd.kernels import linear as lin
         for m in self.modules():
             if isinstance(m, Linear):
                 m.skinny = bool(enabled)
+            elif isinstance(m, GatedMLP) and m._gate_up_blocked:
+                tiled = m._gate_up.dim() == 4
+                if enabled and not tiled:
+                    m._gate_up = lin.tile_weight(m._gate_up)
+                elif not enabled and tiled:
+                    m._gate_up = lin.untile_weight(m._gate_up)
 
     def set_fused_epilogue(self, enabled: bool):
         """Choose, for every attention layer at once, between the fused pre-attention launch

@@ -79,18 +79,20 @@ def test_unsupported_shapes_are_refused():
     assert not supported(x[:8].float(), w.float())
 
 
+@pytest.mark.parametrize("tiled", [False, True], ids=["row-major", "tiled"])
 @pytest.mark.parametrize("m,hid,k", [(64, 14336, 4096), (5, 768, 384), (64, 128, 1024)])
-def test_gated_silu_product_matches_the_separate_bf16_ops(m, hid, k):
+def test_gated_silu_product_matches_the_separate_bf16_ops(m, hid, k, tiled):
     """linear_bf16_gated on the interleaved [W_gate; W_up] against torch's silu(g) * u of the
     kernel's own bf16 products g = x W_gate^T, u = x W_up^T (one K split, so the same fp32 sums):
     within one bf16 rounding (torch's exp and this kernel's may differ in the last fp32 bit)."""
-    from modelcore_amd.kernels.linear import interleave_gate_up, linear_bf16_gated
-    _note("linear gated", m, hid, k)
+    from modelcore_amd.kernels.linear import interleave_gate_up, linear_bf16_gated, tile_weight
+    _note("linear gated", m, hid, k, tiled)
     g = torch.Generator().manual_seed(m + hid + k)
     x = torch.randn(m, k, generator=g).to(torch.bfloat16).to(DEV)
     wg = (torch.randn(hid, k, generator=g) * k ** -0.5).to(torch.bfloat16).to(DEV)
     wu = (torch.randn(hid, k, generator=g) * k ** -0.5).to(torch.bfloat16).to(DEV)
-    h = linear_bf16_gated(x, interleave_gate_up(wg, wu))
+    w = interleave_gate_up(wg, wu)
+    h = linear_bf16_gated(x, tile_weight(w) if tiled else w)
     gate, up = linear_bf16(x, wg, 1), linear_bf16(x, wu, 1)
     want = (torch.nn.functional.silu(gate.float()).to(torch.bfloat16).float() * up.float())
     err = (h.float() - want).abs()

@@ -257,3 +257,16 @@ def test_interleaved_gate_up_weights_split_back_into_gate_and_up():
     torch.testing.assert_close(up.reshape(3, 5, 192), x @ wu.T, atol=1e-5, rtol=0)
     with pytest.raises(ValueError):
         interleave_gate_up(wg[:100], wu[:100])
+
+
+def test_tiled_weights_round_trip_and_hold_64x128_blocks():
+    """tile_weight stores (n, k) as (n/64, k/128, 64, 128) blocks, block [g][s] being rows
+    64g.., columns 128s..; untile_weight restores the row-major weight exactly (CPU)."""
+    from modelcore_amd.kernels.linear import tile_weight, untile_weight
+    w = torch.arange(192 * 384, dtype=torch.float32).reshape(192, 384)
+    t = tile_weight(w)
+    assert t.shape == (3, 3, 64, 128) and t.is_contiguous()
+    assert torch.equal(t[1, 2], w[64:128, 256:384])
+    assert torch.equal(untile_weight(t), w)
+    with pytest.raises(ValueError):
+        tile_weight(w[:100])
