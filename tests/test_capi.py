@@ -102,3 +102,43 @@ def test_epilogue_rejects_odd_head_dim_half_kv_and_bad_dtype():
                                        fake, fake, 2, 1, 8, 2, 128, 64, 64 * 2 * 128, 1e-6, 1.2,
                                        _ext.BF16, None)
     assert st == _ext.EINVAL and b"token stride" in lib.mcamd_last_error()
+
+
+def test_decode_loop_entry_points_reject_bad_shapes_before_any_launch():
+    """The skinny GEMM family, the residual step and the partials epilogue refuse unsupported
+    shapes and null buffers on the host, each with a message naming the problem."""
+    lib = _ext.lib()
+    fake = 1 << 20  # never dereferenced: the checks fail first
+    # skinny GEMM: rows, n / k granularity, split range
+    assert lib.mcamd_linear_bf16(fake, 512, fake, fake, 64, 65, 64, 512, 1, None, 0, None) \
+        == _ext.EUNSUPPORTED and b"at most 64" in lib.mcamd_last_error()
+    assert lib.mcamd_linear_bf16(fake, 512, fake, fake, 96, 4, 96, 512, 1, None, 0, None) \
+        == _ext.EUNSUPPORTED and b"multiple of 64" in lib.mcamd_last_error()
+    assert lib.mcamd_linear_bf16(fake, 512, fake, fake, 64, 4, 64, 512, 8, None, 0, None) \
+        == _ext.EUNSUPPORTED and b"128 * k_splits" in lib.mcamd_last_error()
+    assert lib.mcamd_linear_bf16(fake, 512, fake, fake, 64, 4, 64, 512, 2, None, 0, None) \
+        == _ext.EWORKSPACE
+    assert lib.mcamd_linear_bf16_partials(fake, 512, fake, None, 4, 64, 512, 1, None) \
+        == _ext.EINVAL and b"part" in lib.mcamd_last_error()
+    # gated product: activation and hidden granularity
+    assert lib.mcamd_linear_bf16_gated(fake, 512, fake, fake, 64, 4, 64, 512, 7, 0, None) \
+        == _ext.EUNSUPPORTED and b"silu" in lib.mcamd_last_error()
+    assert lib.mcamd_linear_bf16_gated(fake, 512, fake, fake, 96, 4, 96, 512, _ext.ACT_SILU, 1,
+                                       None) == _ext.EUNSUPPORTED
+    # residual step: exactly one of part / y, n % 8, eps
+    assert lib.mcamd_residual_rmsnorm(fake, fake, 1, fake, fake, fake, 2, 16, 1e-6, None) \
+        == _ext.EINVAL and b"not both" in lib.mcamd_last_error()
+    assert lib.mcamd_residual_rmsnorm(fake, None, 0, fake, fake, fake, 2, 12, 1e-6, None) \
+        == _ext.EINVAL
+    assert lib.mcamd_residual_rmsnorm(fake, None, 0, fake, fake, fake, 2, 16, -1.0, None) \
+        == _ext.EINVAL and b"eps" in lib.mcamd_last_error()
+    assert lib.mcamd_residual_rmsnorm(fake, fake, 0, None, fake, fake, 2, 16, 1e-6, None) \
+        == _ext.EINVAL and b"splits" in lib.mcamd_last_error()
+    # the epilogue on QKV partials: split range and a row narrower than its heads
+    assert lib.mcamd_qk_rope_norm_append_partials(fake, 0, 12 * 128, fake, fake, 64, fake, fake,
+                                                  fake, fake, 2, 1, 8, 2, 128, 64, 64 * 2 * 128,
+                                                  1e-6, 1.2, 1, None) == _ext.EINVAL
+    assert lib.mcamd_qk_rope_norm_append_partials(fake, 2, 10 * 128, fake, fake, 64, fake, fake,
+                                                  fake, fake, 2, 1, 8, 2, 128, 64, 64 * 2 * 128,
+                                                  1e-6, 1.2, 1, None) == _ext.EINVAL
+    assert b"token stride" in lib.mcamd_last_error()
