@@ -230,6 +230,7 @@ int mcamd_linear_bf16_partials(const void *x, int64_t ldx, const void *w, float 
  *           or y given in bf16 (part = NULL)
  *   x_out = bf16(x + y)
  *   h_out = bf16(x_out * rsqrt(mean(x_out^2) + eps))   (fp32 arithmetic)
+ * x_out may be x itself (an in-place update of the residual stream); h_out is a buffer of its own.
  * Replaces, in a block (modelcore/components/block.py:54-60), the residual add `x + f(norm(x))`
  * and the RMSNorm that follows it (modelcore/components/norm.py:43-44), plus the split-K sum of
  * the projection that produced f.
