@@ -96,3 +96,19 @@ def test_bad_arguments_are_refused():
                                       out.data_ptr(), 2, 12, EPS, None) < 0
     with pytest.raises(ValueError):
         residual_rmsnorm(x, torch.zeros(2, 8, dtype=torch.bfloat16, device=DEV))
+
+
+def test_the_residual_stream_can_be_updated_in_place():
+    """x_out = x (the documented in-place form) gives the out-of-place result."""
+    from modelcore_amd import _ext
+    _note("residual in place")
+    g = torch.Generator().manual_seed(21)
+    m, n, s = 48, 4096, 4
+    x = torch.randn(m, n, generator=g).to(torch.bfloat16).to(DEV)
+    part = torch.randn(s, m, n, generator=g).to(DEV)
+    want_x, want_h = residual_rmsnorm(x, Partials(part, s, (m, n)))
+    h = torch.empty_like(x)
+    st = _ext.lib().mcamd_residual_rmsnorm(x.data_ptr(), part.data_ptr(), s, None, x.data_ptr(),
+                                           h.data_ptr(), m, n, EPS, _ext.stream_handle(DEV))
+    _ext.check(st, "residual_rmsnorm")
+    assert torch.equal(x, want_x) and torch.equal(h, want_h)
