@@ -12,10 +12,11 @@
 // per CU, fall well short of that.
 //
 // Work split. A unit is (row b, group of four KV heads, group of up to four query heads per KV
-// head). Laid end to end, the units' keys form T = sum_b n_b * units slots (n_b = p_b - lo_b + 1).
-// The grid has a fixed number W of waves (one per SIMD), and wave w takes the slots
-// [w*T/W, (w+1)*T/W): equal bytes for every SIMD whatever the row lengths. A wave's range is one
-// or a few contiguous segments of units. Every wave derives T and its first row from
+// head). Laid end to end, the units form T = sum_b (n_b + C) * units slots (n_b = p_b - lo_b + 1
+// keys, after C key-free lead slots that stand for the cost of starting a segment). The grid
+// has a fixed number of workgroups (one per CU, a wave per SIMD), and workgroup g takes the slots
+// [g*T/NG, (g+1)*T/NG): equal work for every CU whatever the row lengths. A workgroup's range is
+// one or a few contiguous segments of units. Every workgroup derives T and its first row from
 // cache_seqlens itself (a scan over the rows), so nothing is synchronised with the host.
 //
 // Inside a segment, lane (r, c) = (lane / 16, lane % 16) owns KV head 4*group + r and the 16
@@ -61,6 +62,10 @@ constexpr int kMinKeysPerGroup = MCAMD_DECODE_MIN_KEYS;  // fewer workgroups whe
 #define MCAMD_DECODE_RING 2
 #endif
 constexpr int kRing = MCAMD_DECODE_RING;  // tile buffers per wave (kRing - 1 tiles in flight)
+#ifndef MCAMD_DECODE_SEG_COST
+#define MCAMD_DECODE_SEG_COST 96
+#endif
+constexpr int kSegCost = MCAMD_DECODE_SEG_COST;  // key-free lead slots per unit (see unit_span)
 constexpr int kPart = KG * GM * D + 2 * KG * GM;  // floats per partial: o[16][D], (m, l)[16]
 #ifndef MCAMD_MERGE_BATCH
 #define MCAMD_MERGE_BATCH 8
@@ -145,6 +150,13 @@ __device__ __forceinline__ int row_keys(const FusedParams &P, int b, int &lo) {
   return pos - lo + 1;
 }
 
+// Slots a unit of a row with nk keys takes in the work split: kSegCost lead slots that hold no
+// keys, then its nk keys. The lead slots stand for what starting a segment costs a workgroup
+// (refilling the load pipeline, the four-wave merge, the partial's write) in units of one key's
+// streaming time, so a workgroup whose range holds the start of a unit gets fewer keys and
+// finishes with the others.
+__device__ __forceinline__ int unit_span(int nk) { return nk > 0 ? nk + kSegCost : 0; }
+
 // Workgroup owning flattened slot x when T slots are shared out as [g*T/NG, (g+1)*T/NG).
 __device__ __forceinline__ int group_of(int64_t x, int64_t T, int NG) {
   return int(((x + 1) * NG + T - 1) / T - 1);
@@ -172,7 +184,7 @@ __device__ int64_t slots_before(const FusedParams &P, int b_end, int lane) {
   for (int b0 = 0; b0 < b_end; b0 += 64) {
     int lo;
     const int nk = b0 + lane < b_end ? row_keys(P, b0 + lane, lo) : 0;
-    total += shfl_i64(scan_incl_i64(int64_t(nk) * P.n_units, lane), 63);
+    total += shfl_i64(scan_incl_i64(int64_t(unit_span(nk)) * P.n_units, lane), 63);
   }
   return total;
 }
@@ -185,7 +197,7 @@ __device__ void find_row(const FusedParams &P, int64_t x, int lane, int &b, int6
   for (int b0 = 0; b0 < P.B && b < 0; b0 += 64) {
     int lo;
     const int nk = b0 + lane < P.B ? row_keys(P, b0 + lane, lo) : 0;
-    const int64_t tot = int64_t(nk) * P.n_units;
+    const int64_t tot = int64_t(unit_span(nk)) * P.n_units;
     const int64_t incl = scan_incl_i64(tot, lane);
     const uint64_t hit = __builtin_amdgcn_ballot_w64(carry + incl > x);
     if (hit) {
@@ -213,7 +225,7 @@ __device__ void locate(const FusedParams &P, int g, int lane, int64_t &T, int &N
   if (P.B <= 64) {
     int lo;
     const int nk = lane < P.B ? row_keys(P, lane, lo) : 0;
-    const int64_t tot = int64_t(nk) * P.n_units;
+    const int64_t tot = int64_t(unit_span(nk)) * P.n_units;
     const int64_t incl = scan_incl_i64(tot, lane);
     T = shfl_i64(incl, 63);
     NG = int(min(int64_t(P.n_groups), T));
@@ -241,7 +253,7 @@ __device__ int row_geometry(const FusedParams &P, int b, int lane, int64_t &T, i
   if (P.B <= 64) {
     int lo2;
     const int nkl = lane < P.B ? row_keys(P, lane, lo2) : 0;
-    const int64_t tot = int64_t(nkl) * P.n_units;
+    const int64_t tot = int64_t(unit_span(nkl)) * P.n_units;
     const int64_t incl = scan_incl_i64(tot, lane);
     T = shfl_i64(incl, 63);
     Pb = shfl_i64(incl - tot, b);
@@ -268,7 +280,8 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
       for (int i = threadIdx.x; i < P.H * D; i += 256) P.out[int64_t(b) * P.H * D + i] = 0x7fc0;
   }
   // NG <= T active workgroups: every range [g*T/NG, (g+1)*T/NG) is then non-empty, so the
-  // workgroups spanning a unit are exactly those from its first slot's owner to its last.
+  // workgroups holding a unit's keys are exactly those from its first key's owner to its last
+  // key's (a range of lead slots alone holds no key of the unit and writes nothing for it).
   int64_t T, start = 0, end = 0, Pb = 0;
   int NG, b = 0;
   locate(P, g, lane, T, NG, start, end, b, Pb);
@@ -280,10 +293,16 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
   while (x < end) {
     int lo;
     const int nk = row_keys(P, b, lo);
+    const int span = unit_span(nk);
     const int pos = lo + nk - 1;
     const int64_t off = x - Pb;
-    const int unit = int(off / nk);
-    const int t_rel = int(off - int64_t(unit) * nk);
+    const int unit = int(off / span);
+    const int lead = int(off - int64_t(unit) * span);
+    if (lead < kSegCost) {  // the unit's lead slots: no keys to stream
+      x += kSegCost - lead;
+      continue;
+    }
+    const int t_rel = lead - kSegCost;
     const int seg = int(min(end - x, int64_t(nk - t_rel)));
     const int ts = lo + t_rel;  // first key of the segment
     const int last = ts + seg - 1;
@@ -485,7 +504,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
     };
 
     const int ug = b * P.n_units + unit;
-    const int64_t unit_start = Pb + int64_t(unit) * nk;
+    const int64_t unit_start = Pb + int64_t(unit) * span + kSegCost;  // slot of its first key
     const int g_first = group_of(unit_start, T, NG);
     const int g_last = group_of(unit_start + nk - 1, T, NG);
     if (g_first == g_last) {
@@ -503,7 +522,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
 
     // Next segment: the next unit of this row, or the next row that has keys.
     x += seg;
-    if (x == Pb + int64_t(nk) * P.n_units) {
+    if (x == Pb + int64_t(span) * P.n_units) {
       Pb = x;
       int lo2;
       do {
@@ -530,7 +549,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(FusedParams P) {
   int NG, lo;
   const int nk = row_geometry(P, b, lane, T, NG, Pb, lo);
   if (nk == 0) return;
-  const int64_t unit_start = Pb + int64_t(unit) * nk;
+  const int64_t unit_start = Pb + int64_t(unit) * unit_span(nk) + kSegCost;  // its first key
   const int g_first = group_of(unit_start, T, NG);
   const int nseg = group_of(unit_start + nk - 1, T, NG) - g_first + 1;
   if (nseg == 1) return;  // written directly by the streaming pass
