@@ -113,13 +113,17 @@ def bench_prefill(args):
     cache = KVCache(PF_B, PF_HKV, PF_T, D, 1, dev, torch.bfloat16)
     kc, vc = cache.get_slot_cache(0)
     n_chunks = PF_T // PF_C
+    # Each chunk's q/k/v as its own contiguous (B, C, heads, D) tensor, as an attention layer's
+    # projections hand them to the operator (slices of the whole-prompt tensors would make the
+    # operator copy them first).
+    chunks = [tuple(t[:, c * PF_C:(c + 1) * PF_C].contiguous() for t in (q, k, v))
+              for c in range(n_chunks)]
 
     def one_pass():
         cache.reset()
-        for c in range(n_chunks):
-            a = c * PF_C
-            flash_attn.flash_attn_with_kvcache(q[:, a:a + PF_C], kc, vc, k=k[:, a:a + PF_C],
-                                               v=v[:, a:a + PF_C], cache_seqlens=cache.cache_seqlens,
+        for qc, kc_new, vc_new in chunks:
+            flash_attn.flash_attn_with_kvcache(qc, kc, vc, k=kc_new, v=vc_new,
+                                               cache_seqlens=cache.cache_seqlens,
                                                causal=True, window_size=(-1, 0))
             cache.advance(PF_C)
 
@@ -139,7 +143,7 @@ def bench_prefill(args):
     lib = _ext.lib()
     out = torch.empty(PF_B, PF_C, PF_H, D, dtype=torch.bfloat16, device=dev)
     offs = [torch.full((PF_B,), c * PF_C, dtype=torch.int32, device=dev) for c in range(n_chunks)]
-    qs = [q[:, c * PF_C:(c + 1) * PF_C].contiguous() for c in range(n_chunks)]
+    qs = [qc for qc, _, _ in chunks]
     stream = _ext.stream_handle(dev)
 
     def attn_pass():
