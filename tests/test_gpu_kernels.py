@@ -145,6 +145,9 @@ def _oracle(c, window, with_append=True):
     return ko.flash_attn_with_kvcache(q, kc, vc, k, v, c["cache_seqlens"].tolist(), window)[0]
 
 
+# 80 ragged rows: past 64 rows the fused kernel's work split scans cache_seqlens in chunks of 64.
+RAGGED_80 = [int(x) for x in np.random.default_rng(5).integers(0, 650, 80)]
+
 DECODE_CASES = [
     # seqlens, H, H_kv, D, T_max, window
     ([37, 300, 0, 511], 16, 4, 128, 520, -1),
@@ -160,6 +163,8 @@ DECODE_CASES = [
     ([4095, 17], 4, 4, 128, 4100, 1024),    # MHA, 4 windowed splits
     ([0, 3], 16, 4, 128, 2000, -1),         # far fewer keys than waves
     ([1999, 0, 1], 16, 4, 128, 2000, 5),    # tiny windows in a long cache
+    (RAGGED_80, 16, 4, 128, 700, -1),       # more rows than one wave scans
+    (RAGGED_80, 16, 4, 128, 700, 100),
 ]
 
 
