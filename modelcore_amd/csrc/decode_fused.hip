@@ -139,6 +139,18 @@ struct Tile {
   uint4 k[kTokens], v[kTokens];
 };
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// An empty use of a tile's registers: they stay allocated to it (and any load into them is
+// waited for) up to this point, which comes after `anchor` is computed and before it is used.
+__device__ __forceinline__ void keep_tile(const Tile &t, float &anchor) {
+  asm volatile("" : "+v"(anchor)
+               : "v"(__builtin_bit_cast(u32x4, t.k[0])), "v"(__builtin_bit_cast(u32x4, t.k[1])),
+               "v"(__builtin_bit_cast(u32x4, t.k[2])), "v"(__builtin_bit_cast(u32x4, t.k[3])),
+               "v"(__builtin_bit_cast(u32x4, t.v[0])), "v"(__builtin_bit_cast(u32x4, t.v[1])),
+               "v"(__builtin_bit_cast(u32x4, t.v[2])), "v"(__builtin_bit_cast(u32x4, t.v[3])));
+}
+
 // Keys of row b (the range [lo, pos]), or 0 for a row whose position is outside the cache.
 __device__ __forceinline__ int row_keys(const FusedParams &P, int b, int &lo) {
   const int pos = P.seqlens[b];
@@ -156,6 +168,15 @@ __device__ __forceinline__ int row_keys(const FusedParams &P, int b, int &lo) {
 // streaming time, so a workgroup whose range holds the start of a unit gets fewer keys and
 // finishes with the others.
 __device__ __forceinline__ int unit_span(int nk) { return nk > 0 ? nk + kSegCost : 0; }
+
+// A workgroup barrier that orders LDS accesses only. __syncthreads() also fences global memory,
+// which here would make every wave wait, at each segment's end, for its prefetch past the
+// segment (one memory latency); the waves of a workgroup share nothing through global memory.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // Workgroup owning flattened slot x when T slots are shared out as [g*T/NG, (g+1)*T/NG).
 __device__ __forceinline__ int group_of(int64_t x, int64_t T, int NG) {
@@ -461,7 +482,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
       mine.m[r][c] = m;
       mine.l[r][c] = l;
     }
-    __syncthreads();
+    lds_barrier();
 
     // Merge the four waves: wave wv now owns KV-head row wv; lane (h, c) = (lane / 16, lane % 16)
     // owns head h and dims c*8..c*8+7 of that row.
@@ -503,6 +524,12 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
       *reinterpret_cast<uint4 *>(out_at) = v4;
     };
 
+    // The ring's registers stay allocated to it up to here, after the four-wave merge: the
+    // loads of the tile prefetched past the segment may still be in flight, and code that
+    // reused those registers earlier would have to wait for them first.
+#pragma unroll
+    for (int i = 0; i < kRing; ++i) keep_tile(ring[i], acc[0]);
+
     const int ug = b * P.n_units + unit;
     const int64_t unit_start = Pb + int64_t(unit) * span + kSegCost;  // slot of its first key
     const int g_first = group_of(unit_start, T, NG);
@@ -518,7 +545,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
       *reinterpret_cast<float4 *>(po + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
       if (c == 0) *reinterpret_cast<float2 *>(slot + KG * GM * D + 2 * (mr * GM + mh)) = make_float2(M, L);
     }
-    __syncthreads();  // s_acc is reused by the next segment
+    lds_barrier();  // s_acc is reused by the next segment
 
     // Next segment: the next unit of this row, or the next row that has keys.
     x += seg;
