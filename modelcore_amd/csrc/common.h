@@ -64,6 +64,15 @@ __device__ __forceinline__ uint4 load_stream(const void *p) {
   return __builtin_bit_cast(uint4, __builtin_nontemporal_load(static_cast<const u32x4_nt *>(p)));
 }
 
+// A workgroup barrier that orders LDS accesses only. __syncthreads() also fences global memory,
+// so the waves first wait for every global load and store they have in flight; where a
+// workgroup's waves share nothing through global memory, that wait is pure latency.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // A 16-byte vector of elements: 8 x bf16 or 4 x fp32. All kernels move data in these units.
 template <class E> struct Vec;
 

@@ -169,15 +169,6 @@ __device__ __forceinline__ int row_keys(const FusedParams &P, int b, int &lo) {
 // finishes with the others.
 __device__ __forceinline__ int unit_span(int nk) { return nk > 0 ? nk + kSegCost : 0; }
 
-// A workgroup barrier that orders LDS accesses only. __syncthreads() also fences global memory,
-// which here would make every wave wait, at each segment's end, for its prefetch past the
-// segment (one memory latency); the waves of a workgroup share nothing through global memory.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Workgroup owning flattened slot x when T slots are shared out as [g*T/NG, (g+1)*T/NG).
 __device__ __forceinline__ int group_of(int64_t x, int64_t T, int NG) {
   return int(((x + 1) * NG + T - 1) / T - 1);
@@ -482,7 +473,8 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
       mine.m[r][c] = m;
       mine.l[r][c] = l;
     }
-    lds_barrier();
+    lds_barrier();  // not __syncthreads(): its global fence would wait for the prefetch past
+                    // the segment; the waves share nothing through global memory
 
     // Merge the four waves: wave wv now owns KV-head row wv; lane (h, c) = (lane / 16, lane % 16)
     // owns head h and dims c*8..c*8+7 of that row.

@@ -18,6 +18,7 @@ namespace mcamd {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kMaxBatchedSplits = 4;  // partial counts whose loads are issued together
 
 struct ResParams {
   const uint16_t *x, *y;
@@ -48,7 +49,10 @@ __device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
 
 // CPT > 0: each thread keeps its (at most CPT) chunks of x_out in registers for the norm;
 // CPT = 0: any row length, the norm pass re-reads the thread's own chunks of x_out.
-template <int CPT>
+// MAXS > 0 (at most MAXS partials): the partial loads of all the thread's chunks are issued
+// before the first is summed, so they cost one memory latency, not one per partial and chunk;
+// MAXS = 0: any number of partials, loaded one after the other.
+template <int CPT, int MAXS>
 __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(ResParams P) {
   __shared__ float wsum[kThreads / 64];
   const int m = blockIdx.x;
@@ -57,22 +61,66 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(ResParams P)
   constexpr int kHeld = CPT > 0 ? CPT : 1;
   float held[kHeld][8];
   float ss = 0.f;
-  auto residual_chunk = [&](int c, float (&sv)[8]) {
-    float xv[8], yv[8];
-    unpack8(*reinterpret_cast<const uint4 *>(P.x + row + 8 * c), xv);
+  // A chunk's inputs: x, and y or (with MAXS > 0) the partials. All of a thread's chunks are
+  // loaded before the first is summed and stored (x_out may be x itself, so the compiler would
+  // not move a later chunk's loads above an earlier chunk's store on its own).
+  constexpr int kS = MAXS > 0 ? MAXS : 1;
+  uint4 xin[kHeld], yin[kHeld];
+  float4 pa[kHeld][kS], pb[kHeld][kS];
+  auto slice = [&](int s, int c) {
+    return reinterpret_cast<const float4 *>(P.part + int64_t(s) * P.M * P.N + row + 8 * c);
+  };
+  // The loads of chunk c into slot u. With MAXS > 0 the last partial stands in for absent ones
+  // (the sum skips them), so every load issues here.
+  auto load_x = [&](int c, int u) { xin[u] = *reinterpret_cast<const uint4 *>(P.x + row + 8 * c); };
+  auto load_y = [&](int c, int u) { yin[u] = *reinterpret_cast<const uint4 *>(P.y + row + 8 * c); };
+  auto load_parts = [&](int c, int u) {
+    if constexpr (MAXS > 0) {
+#pragma unroll
+      for (int s = 0; s < MAXS; ++s) {
+        const float4 *q = slice(min(s, P.S - 1), c);
+        pa[u][s] = q[0], pb[u][s] = q[1];
+      }
+    }
+  };
+  // All slots' loads, unconditional (a slot past the row re-reads its last chunk) and in one
+  // block per input kind, so that no arithmetic is scheduled between them.
+  auto load_all = [&]() {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) load_x(min(int(threadIdx.x) + u * kThreads, chunks - 1), u);
     if (P.part) {
+#pragma unroll
+      for (int u = 0; u < CPT; ++u) load_parts(min(int(threadIdx.x) + u * kThreads, chunks - 1), u);
+    } else {
+#pragma unroll
+      for (int u = 0; u < CPT; ++u) load_y(min(int(threadIdx.x) + u * kThreads, chunks - 1), u);
+    }
+  };
+  auto residual_chunk = [&](int c, int u, float (&sv)[8]) {
+    float xv[8], yv[8];
+    unpack8(xin[u], xv);
+    if (P.part) {
+      // The in-order fp32 sum of the partials, as the GEMM's own reduce pass makes it.
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int s = 0; s < P.S; ++s) {
-        const float4 *p = reinterpret_cast<const float4 *>(P.part + int64_t(s) * P.M * P.N + row +
-                                                           8 * c);
-        const float4 a = p[0], b = p[1];
-        acc[0] += a.x, acc[1] += a.y, acc[2] += a.z, acc[3] += a.w;
-        acc[4] += b.x, acc[5] += b.y, acc[6] += b.z, acc[7] += b.w;
+      if constexpr (MAXS > 0) {
+#pragma unroll
+        for (int s = 0; s < MAXS; ++s) {
+          if (s < P.S) {
+            acc[0] += pa[u][s].x, acc[1] += pa[u][s].y, acc[2] += pa[u][s].z, acc[3] += pa[u][s].w;
+            acc[4] += pb[u][s].x, acc[5] += pb[u][s].y, acc[6] += pb[u][s].z, acc[7] += pb[u][s].w;
+          }
+        }
+      } else {
+        for (int s = 0; s < P.S; ++s) {
+          const float4 a = slice(s, c)[0], b = slice(s, c)[1];
+          acc[0] += a.x, acc[1] += a.y, acc[2] += a.z, acc[3] += a.w;
+          acc[4] += b.x, acc[5] += b.y, acc[6] += b.z, acc[7] += b.w;
+        }
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) yv[i] = __uint_as_float(uint32_t(to_bf16(acc[i])) << 16);
     } else {
-      unpack8(*reinterpret_cast<const uint4 *>(P.y + row + 8 * c), yv);
+      unpack8(yin[u], yv);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -82,18 +130,26 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(ResParams P)
     *reinterpret_cast<uint4 *>(P.x_out + row + 8 * c) = pack8(sv);
   };
   if constexpr (CPT > 0) {
+    load_all();
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
       const int c = threadIdx.x + u * kThreads;
-      if (c < chunks) residual_chunk(c, held[u]);
+      if (c < chunks) residual_chunk(c, u, held[u]);
     }
   } else {
-    for (int c = threadIdx.x; c < chunks; c += kThreads) residual_chunk(c, held[0]);
+    for (int c = threadIdx.x; c < chunks; c += kThreads) {
+      load_x(c, 0);
+      if (P.part)
+        load_parts(c, 0);
+      else
+        load_y(c, 0);
+      residual_chunk(c, 0, held[0]);
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
   if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = ss;
-  __syncthreads();
+  lds_barrier();  // the x_out stores above need not land before the norm's sum is shared
   float total = 0.f;
 #pragma unroll
   for (int w = 0; w < kThreads / 64; ++w) total += wsum[w];
@@ -154,13 +210,16 @@ extern "C" int mcamd_residual_rmsnorm(const void *x, const float *part, int64_t 
   const int64_t chunks = n / 8;
   const dim3 grid{unsigned(m), 1, 1}, block{unsigned(kThreads), 1, 1};
   hipStream_t s = as_stream(stream);
-  if (chunks <= kThreads)
-    hipLaunchKernelGGL(residual_rmsnorm_kernel<1>, grid, block, 0, s, P);
-  else if (chunks <= 2 * kThreads)
-    hipLaunchKernelGGL(residual_rmsnorm_kernel<2>, grid, block, 0, s, P);
-  else if (chunks <= 4 * kThreads)
-    hipLaunchKernelGGL(residual_rmsnorm_kernel<4>, grid, block, 0, s, P);
-  else
-    hipLaunchKernelGGL(residual_rmsnorm_kernel<0>, grid, block, 0, s, P);
+  if (P.S > kMaxBatchedSplits) {
+    hipLaunchKernelGGL((residual_rmsnorm_kernel<0, 0>), grid, block, 0, s, P);
+  } else if (chunks <= kThreads) {
+    hipLaunchKernelGGL((residual_rmsnorm_kernel<1, kMaxBatchedSplits>), grid, block, 0, s, P);
+  } else if (chunks <= 2 * kThreads) {
+    hipLaunchKernelGGL((residual_rmsnorm_kernel<2, kMaxBatchedSplits>), grid, block, 0, s, P);
+  } else if (chunks <= 4 * kThreads) {
+    hipLaunchKernelGGL((residual_rmsnorm_kernel<4, kMaxBatchedSplits>), grid, block, 0, s, P);
+  } else {
+    hipLaunchKernelGGL((residual_rmsnorm_kernel<0, kMaxBatchedSplits>), grid, block, 0, s, P);
+  }
   return launch_status("residual_rmsnorm");
 }
