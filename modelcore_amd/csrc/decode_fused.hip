@@ -34,7 +34,9 @@
 //  * Output: a segment that covers its whole unit writes the normalised output; otherwise it
 //    writes (o, m, l) for its 16 heads to workspace slot wave + unit (distinct per segment, since
 //    units advance with the waves), and the merge pass -- one wave per (unit, query head), lane
-//    l owning dims 2l and 2l + 1 -- combines a unit's segments by log-sum-exp.
+//    l owning dims 2l and 2l + 1 -- combines a unit's segments by log-sum-exp. The workgroup
+//    holding a unit's first key records the unit's (first workgroup, segment count), so the
+//    merge pass finds the partials without rebuilding the work split.
 //  * Append: the segment that ends at p reads the new token from k/v instead of the cache and
 //    its lanes store it into the cache at p (bit-exact copy; the first query-head group only).
 #include "kernels.h"
@@ -81,6 +83,7 @@ struct FusedParams {
   const int32_t *seqlens;
   uint16_t *out;
   float *part;  // [n_groups + B * n_units][kPart]: segment partials, slot = group + unit
+  int2 *desc;   // [B * n_units]: (first workgroup, segments) of each unit that has keys
   int B, H, H_kv, G, n_hc, n_kg, n_units, T_max, window, n_groups;
   int64_t cache_b;
   float scale_log2;
@@ -255,26 +258,6 @@ __device__ void locate(const FusedParams &P, int g, int lane, int64_t &T, int &N
   start = int64_t(g) * T / NG;
   end = int64_t(g + 1) * T / NG;
   find_row(P, start, lane, b, Pb);
-}
-
-// Geometry of row b for the merge pass: total slots T, active workgroups NG, first slot Pb of
-// row b and its key range start lo; returns the row's key count (0: nothing to merge).
-__device__ int row_geometry(const FusedParams &P, int b, int lane, int64_t &T, int &NG,
-                            int64_t &Pb, int &lo) {
-  const int nk = row_keys(P, b, lo);
-  if (P.B <= 64) {
-    int lo2;
-    const int nkl = lane < P.B ? row_keys(P, lane, lo2) : 0;
-    const int64_t tot = int64_t(unit_span(nkl)) * P.n_units;
-    const int64_t incl = scan_incl_i64(tot, lane);
-    T = shfl_i64(incl, 63);
-    Pb = shfl_i64(incl - tot, b);
-  } else {
-    T = slots_before(P, P.B, lane);
-    Pb = slots_before(P, b, lane);
-  }
-  NG = int(min(int64_t(P.n_groups), T));
-  return nk;
 }
 
 __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
@@ -526,6 +509,9 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
     const int64_t unit_start = Pb + int64_t(unit) * span + kSegCost;  // slot of its first key
     const int g_first = group_of(unit_start, T, NG);
     const int g_last = group_of(unit_start + nk - 1, T, NG);
+    // The workgroup holding the unit's first key tells the merge pass where the unit's
+    // partials are, so that it need not rebuild the work split from cache_seqlens.
+    if (g == g_first && threadIdx.x == 0) P.desc[ug] = make_int2(g_first, g_last - g_first + 1);
     if (g_first == g_last) {
       if (m_live) write_out(acc, L);  // the segment is the whole unit
     } else {
@@ -565,13 +551,12 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(FusedParams P) {
   const int kvh = kg * KG + hr / GM;
   const int hh = hr % GM;
   if (kvh >= P.H_kv || hh >= min(GM, P.G - hc * GM)) return;
-  int64_t T, Pb;
-  int NG, lo;
-  const int nk = row_geometry(P, b, lane, T, NG, Pb, lo);
-  if (nk == 0) return;
-  const int64_t unit_start = Pb + int64_t(unit) * unit_span(nk) + kSegCost;  // its first key
-  const int g_first = group_of(unit_start, T, NG);
-  const int nseg = group_of(unit_start + nk - 1, T, NG) - g_first + 1;
+  // The unit's (first workgroup, segments), published by the streaming pass; a row outside
+  // the cache has no keys and no descriptor (its NaN output is written), so it is checked too.
+  int lo;
+  const int2 d = P.desc[ug];
+  if (row_keys(P, b, lo) == 0) return;
+  const int g_first = d.x, nseg = d.y;
   if (nseg == 1) return;  // written directly by the streaming pass
   const float *base = P.part + int64_t(g_first + ug) * kPart;
   float M = -INFINITY, L = 0.f, t0 = 0.f, t1 = 0.f;
@@ -624,7 +609,8 @@ size_t decode_fused_partial_bytes(int64_t batch, int64_t n_head, int64_t n_kv_he
                                   int64_t t_max, int64_t window) {
   (void)t_max;
   (void)window;
-  return size_t((kMaxGroups + batch * decode_fused_units(n_head, n_kv_head)) * kPart * 4);
+  const int64_t units = batch * decode_fused_units(n_head, n_kv_head);
+  return size_t((kMaxGroups + units) * kPart * 4 + units * int64_t(sizeof(int2)));
 }
 
 bool decode_fused_supported(const AttnArgs &a) {
@@ -660,6 +646,7 @@ int launch_decode_fused(const AttnArgs &a) {
   P.n_groups = int(groups);
   char *ws = static_cast<char *>(a.workspace);
   P.part = reinterpret_cast<float *>(ws + kCounterRegionBytes);
+  P.desc = reinterpret_cast<int2 *>(P.part + (kMaxGroups + int64_t(P.B) * P.n_units) * kPart);
   hipLaunchKernelGGL(decode_fused_kernel, dim3(unsigned(groups)), dim3(256), 0, a.stream, P);
   int st = launch_status("decode_fused");
   if (st != MCAMD_OK) return st;
