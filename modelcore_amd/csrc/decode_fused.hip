@@ -85,6 +85,7 @@ struct FusedParams {
   float *part;  // [n_groups + B * n_units][kPart]: segment partials, slot = group + unit
   int2 *desc;   // [B * n_units]: (first workgroup, segments) of each unit that has keys
   int B, H, H_kv, G, n_hc, n_kg, n_units, T_max, window, n_groups;
+  int scan32;  // B <= 64 and every sum of row slot counts fits in 31 bits
   int64_t cache_b;
   float scale_log2;
 };
@@ -184,6 +185,19 @@ __device__ __forceinline__ int64_t shfl_i64(int64_t v, int src) {
   return int64_t((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
 }
 
+// Inclusive prefix sum over the 64 lanes in 32 bits, with DPP: shifts by 1, 2, 4, 8 within each
+// row of 16 lanes, then the last lane of row r added to row r + 1 (row_bcast:15) and the last
+// lane of row 1 to rows 2 and 3 (row_bcast:31); lanes with no source add 0.
+__device__ __forceinline__ int scan_incl_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return v;
+}
+
 __device__ __forceinline__ int64_t scan_incl_i64(int64_t v, int lane) {
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
@@ -237,6 +251,21 @@ struct WaveAcc {
 // cache_seqlens when B <= 64.
 __device__ void locate(const FusedParams &P, int g, int lane, int64_t &T, int &NG, int64_t &start,
                        int64_t &end, int &b, int64_t &Pb) {
+  if (P.scan32) {
+    int lo;
+    const int nk = lane < P.B ? row_keys(P, lane, lo) : 0;
+    const int tot = unit_span(nk) * P.n_units;
+    const int incl = scan_incl_i32(tot);
+    T = __builtin_amdgcn_readlane(incl, 63);
+    NG = int(min(int64_t(P.n_groups), T));
+    if (g >= NG) return;
+    start = int64_t(g) * T / NG;
+    end = int64_t(g + 1) * T / NG;
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(incl > start);
+    b = __builtin_ctzll(hit);
+    Pb = __builtin_amdgcn_readlane(incl - tot, b);
+    return;
+  }
   if (P.B <= 64) {
     int lo;
     const int nk = lane < P.B ? row_keys(P, lane, lo) : 0;
@@ -637,6 +666,9 @@ int launch_decode_fused(const AttnArgs &a) {
   P.T_max = int(a.t_max);
   P.window = int(a.window < 0 ? -1 : a.window);
   P.cache_b = a.cache_batch_stride;
+  // Row slot counts are at most (T_max + kSegCost) * n_units each.
+  P.scan32 = a.batch <= 64 &&
+             a.batch * P.n_units * (a.t_max + int64_t(kSegCost)) < (int64_t(1) << 31);
   P.scale_log2 = float(kLog2e / std::sqrt(double(D)));
   // Workgroups: one per CU, but no more than one per kMinKeysPerGroup slots of the largest total.
   const int64_t span = a.window >= 0 ? std::min<int64_t>(a.t_max, a.window + 1) : a.t_max;
