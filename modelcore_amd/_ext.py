@@ -132,12 +132,12 @@ _RETIRED: list[torch.Tensor] = []
 def workspace(device, nbytes: int):
     """A device buffer of at least `nbytes` for the attention entry points, or None for 0.
 
-    The decode kernels keep merge counters at the start of the workspace: it must be zero when
-    first handed over, and every call leaves it that way. So one zero-filled buffer per device is
-    kept and reused by every call issued on that device's stream (calls on two streams at once
-    would share it and race). A buffer that is outgrown is retired but kept alive, so a graph
-    captured with it stays valid. During graph capture a too-small buffer is not replaced:
-    the call gets a zero-filled buffer of its own from the graph's pool.
+    The workspace is scratch: a call needs no particular contents in it and leaves none that a
+    later call relies on. One buffer per device is kept and reused by every call issued on that
+    device's stream (calls on two streams at once would share it and race). A buffer that is
+    outgrown is retired but kept alive, so a graph captured with it stays valid. During graph
+    capture a too-small buffer is not replaced: the call gets one of its own from the graph's
+    pool.
     """
     if nbytes == 0:
         return None
@@ -146,11 +146,11 @@ def workspace(device, nbytes: int):
     if ws is not None and ws.numel() >= nbytes:
         return ws
     if torch.cuda.is_current_stream_capturing():
-        return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
     size = max(nbytes, 2 * ws.numel() if ws is not None else 0, 1 << 20)
     if ws is not None:
         _RETIRED.append(ws)
-    ws = torch.zeros(size, dtype=torch.uint8, device=device)
+    ws = torch.empty(size, dtype=torch.uint8, device=device)
     _WORKSPACES[idx] = ws
     return ws
 

@@ -643,8 +643,9 @@ size_t decode_fused_partial_bytes(int64_t batch, int64_t n_head, int64_t n_kv_he
 }
 
 bool decode_fused_supported(const AttnArgs &a) {
+  // The merge grid has one wave per (unit, query head of a unit): it must fit a 32-bit grid.
   return a.dtype == MCAMD_BF16 && a.head_dim == D &&
-         a.batch * decode_fused_units(a.n_head, a.n_kv_head) <= kMaxCounters;
+         a.batch * decode_fused_units(a.n_head, a.n_kv_head) * KG * GM < (int64_t(1) << 31);
 }
 
 int launch_decode_fused(const AttnArgs &a) {
@@ -677,7 +678,7 @@ int launch_decode_fused(const AttnArgs &a) {
   groups = std::max<int64_t>(1, std::min<int64_t>(groups, (t_upper + kMinKeysPerGroup - 1) / kMinKeysPerGroup));
   P.n_groups = int(groups);
   char *ws = static_cast<char *>(a.workspace);
-  P.part = reinterpret_cast<float *>(ws + kCounterRegionBytes);
+  P.part = reinterpret_cast<float *>(ws);
   P.desc = reinterpret_cast<int2 *>(P.part + (kMaxGroups + int64_t(P.B) * P.n_units) * kPart);
   hipLaunchKernelGGL(decode_fused_kernel, dim3(unsigned(groups)), dim3(256), 0, a.stream, P);
   int st = launch_status("decode_fused");

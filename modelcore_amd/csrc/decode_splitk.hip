@@ -285,7 +285,7 @@ size_t decode_workspace_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, 
   const size_t fused =
       head_dim == 128 ? decode_fused_partial_bytes(batch, n_head, n_kv_head, t_max, window) : 0;
   const size_t part = generic > fused ? generic : fused;
-  return kCounterRegionBytes + (part + 255) / 256 * 256;
+  return (part + 255) / 256 * 256;
 }
 
 int launch_decode(const AttnArgs &a) {
@@ -325,7 +325,7 @@ int launch_decode(const AttnArgs &a) {
   P.scale_log2 = float(kLog2e / std::sqrt(double(a.head_dim)));
   const int64_t floats_o = a.batch * a.n_head * P.n_splits * a.head_dim;
   P.k_new = P.v_new = nullptr;  // appended above
-  P.part_o = reinterpret_cast<float *>(static_cast<char *>(a.workspace) + kCounterRegionBytes);
+  P.part_o = static_cast<float *>(a.workspace);
   P.part_ml = P.part_o + floats_o;
   if (a.dtype == MCAMD_BF16) return dispatch_d<bf16>(P, int(a.batch), a.stream);
   return dispatch_d<float>(P, int(a.batch), a.stream);

@@ -36,10 +36,8 @@ int launch_prefill(const AttnArgs &a);
 constexpr int kDecodeSplitLen = 256;
 int64_t decode_max_splits(int64_t t_max, int64_t window);
 
-// Workspace layout of the decode path: a fixed region of merge counters first (zero when the
-// workspace is handed over, and left zero by every call), then the split partials.
-constexpr size_t kCounterRegionBytes = 64 * 1024;
-constexpr int64_t kMaxCounters = int64_t(kCounterRegionBytes / 4);
+// Workspace of the decode path: scratch for the split partials (and the fused path's per-unit
+// descriptors), written and read within one call; no contents are required on entry.
 size_t decode_workspace_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
                               int64_t t_max, int64_t window);
 

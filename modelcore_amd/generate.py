@@ -103,7 +103,9 @@ class CapturedStep:
     on the host around each replay, without touching the device.
 
     Needs a uniform cache (every row at one position, as after ``KVCache.prefill``): a ragged
-    cache checks its rotary positions with a device read, which a graph cannot hold. The first
+    cache checks its rotary positions with a device read, which a graph cannot hold. Every
+    attention layer must take the fused pre-attention step, which reads its RoPE positions from
+    ``cache_seqlens`` on the device (the separate ops would keep the capture's position). The first
     column is drawn from the decoder's current logits when the step is built, and building runs
     one real step (the warm-up that settles lazily created buffers) before the capture.
     """
@@ -115,6 +117,13 @@ class CapturedStep:
         if cache.uniform_pos() is None:
             raise ValueError("CapturedStep needs a uniform cache (rows at one position)")
         model = decoder.model
+        # The separate RoPE ops slice the tables at the host position of the capture, which a
+        # replay would reuse at every later position; the fused step reads positions on the device.
+        unfused = [b.layer_idx for b in model.body.blocks if not b.mixer.fuses_epilogue(cache)]
+        if unfused:
+            raise ValueError(f"CapturedStep needs every attention layer on the fused pre-attention "
+                             f"step (RoPE at positions read on the device); layers {unfused} run "
+                             f"the separate ops, whose RoPE would stay at the capture's position")
         self._rotary_len = min(b.mixer.rope.cos.size(1) for b in model.body.blocks)
         self.tokens = sampler(decoder.logits, self.temperature).view(-1, 1).clone()
         side = torch.cuda.Stream(device=self.tokens.device)

@@ -21,6 +21,7 @@ so code and tests that set them keep working; they select nothing here.
 """
 from __future__ import annotations
 
+import os
 from types import SimpleNamespace
 
 import torch
@@ -52,6 +53,31 @@ USE_FA3 = _resolve_use_fa3()
 # (modelcore/kernels/flash_attn.py:88-93). The HIP kernels have a single branch for uniform and
 # ragged rows, so the flag changes nothing.
 _force_ragged = False
+
+
+# Checked mode (opt-in): read cache_seqlens back before launching and raise IndexError when a new
+# token's position falls outside [0, T_max), as the reference's cache write does
+# (modelcore/kernels/flash_attn.py:336-346: an index_put past the cache raises). It costs one host
+# sync per call and cannot run under graph capture. Unchecked, such a row is neither appended nor
+# attended: its output is NaN, and the callers in this package check positions on the host side
+# (Model.check_cache_room). Enabled by set_checked(True) or MODELCORE_AMD_CHECK_POSITIONS=1.
+CHECK_POSITIONS = os.environ.get("MODELCORE_AMD_CHECK_POSITIONS", "0") == "1"
+
+
+def set_checked(enabled: bool):
+    """Turn the operator's checked mode on or off (see CHECK_POSITIONS)."""
+    global CHECK_POSITIONS
+    CHECK_POSITIONS = bool(enabled)
+
+
+def _check_positions(seqlens, T_new, T_max):
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("flash_attn_with_kvcache: checked mode reads cache_seqlens on the host "
+                           "and cannot run under graph capture; call set_checked(False) first")
+    lo, hi = (int(x) for x in torch.aminmax(seqlens))
+    if lo < 0 or hi + T_new > T_max:
+        raise IndexError(f"flash_attn_with_kvcache: positions [{lo}, {hi + T_new}) of the new "
+                         f"tokens fall outside the cache of {T_max} positions")
 
 
 def hip_load_error():
@@ -140,6 +166,8 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
             raise TypeError(f"{name} is {t.dtype}, q is {dt}")
     code = _ext.dtype_code(dt)
     seqlens = _check_seqlens(cache_seqlens, B, q.device)
+    if CHECK_POSITIONS and B > 0:
+        _check_positions(seqlens, T_new, T_max)
     q = q.contiguous()
     if k is not None:
         k, v = k.contiguous(), v.contiguous()

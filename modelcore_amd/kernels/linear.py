@@ -27,6 +27,7 @@ WIDE_N = 192 * 128  # from this N on, 128-row tiles of eight waves with no K spl
 STAGE_K = 128   # k per pipeline stage
 _CUS = 256
 _WS: dict = {}
+_RETIRED: list = []  # outgrown workspaces, kept alive: a captured graph may still write to them
 
 
 def supported(x: torch.Tensor, w: torch.Tensor) -> bool:
@@ -57,15 +58,24 @@ def k_splits(m: int, n: int, k: int) -> int:
 
 
 def _workspace(device, nbytes):
+    """The split-K partials buffer of this device, at least `nbytes` (None for 0).
+
+    One buffer per device is shared by every call on that device's stream. A graph captured with
+    it holds its address, so an outgrown buffer is retired but kept alive (never returned to the
+    caching allocator, whose next tensor would otherwise receive the graph's writes). During
+    capture a too-small buffer is not replaced: the call gets one of the graph's own pool."""
     if nbytes == 0:
         return None
     idx = device.index if device.index is not None else torch.cuda.current_device()
     ws = _WS.get(idx)
     if ws is not None and ws.numel() >= nbytes:
         return ws
-    if torch.cuda.is_current_stream_capturing():  # a buffer of the graph's own pool
+    if torch.cuda.is_current_stream_capturing():
         return torch.empty(nbytes, dtype=torch.uint8, device=device)
-    ws = _WS[idx] = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+    size = max(nbytes, 2 * ws.numel() if ws is not None else 0, 1 << 20)
+    if ws is not None:
+        _RETIRED.append(ws)
+    ws = _WS[idx] = torch.empty(size, dtype=torch.uint8, device=device)
     return ws
 
 

@@ -334,10 +334,16 @@ class Attention(nn.Module):
         from modelcore_amd.kernels import linear as lin
         return lin.linear_bf16_partials(x, self._qkv) if lin.supported(x, self._qkv) else None
 
+    def fuses_epilogue(self, kv_cache):
+        """Whether forward() with this cache takes the fused pre-attention step, whose RoPE reads
+        each row's position from cache_seqlens on the device (the separate ops slice the tables
+        at the host-side position instead)."""
+        return kv_cache is not None and self.epilogue is not None and self.fuse_epilogue \
+            and isinstance(self.norm, RMSNorm)
+
     def forward(self, x, kv_cache, kv_bus):
         B, T, _ = x.size()
-        fused = kv_cache is not None and self.epilogue is not None and self.fuse_epilogue \
-            and isinstance(self.norm, RMSNorm)
+        fused = self.fuses_epilogue(kv_cache)
         if fused:
             part = self._qkv_partials(x)
             if part is not None:
@@ -742,9 +748,22 @@ class Model(nn.Module):
     def get_device(self):
         return next(self.parameters()).device
 
+    @staticmethod
+    def check_cache_room(kv_cache, T):
+        """T more positions must fit in the cache: the reference fails at the cache write
+        (an index error past T_max), which the kernels cannot raise, so the check is made here
+        -- free on a uniform cache (the host mirror), one host read on a ragged one (as the
+        ragged RoPE gather makes anyway)."""
+        pos = kv_cache.uniform_pos()
+        last = pos + T if pos is not None else int(kv_cache.cache_seqlens.max().item()) + T
+        assert last <= kv_cache.max_seq_len, \
+            f"Sequence length {last} exceeds cache length {kv_cache.max_seq_len}"
+
     def forward(self, idx, targets=None, kv_cache=None):
         if targets is not None:
             raise NotImplementedError("training loss is not part of the inference path")
+        if kv_cache is not None:
+            self.check_cache_room(kv_cache, idx.size(1))
         x = self.embedding(idx)
         x, h = self.body.forward_carry(x, kv_cache)
         if kv_cache is not None:
@@ -755,6 +774,7 @@ class Model(nn.Module):
         """forward(), but the head runs only at position last[b] of row b: (B, vocab) logits.
         The head is per position, so these equal forward()[b, last[b]]; a prompt prefill needs
         only its last position, and skips the (B, T, vocab) logits of all the others."""
+        self.check_cache_room(kv_cache, idx.size(1))
         x, h = self.body.forward_carry(self.embedding(idx), kv_cache)
         kv_cache.advance(idx.size(1))
         rows = torch.arange(idx.size(0), device=x.device)

@@ -1,0 +1,178 @@
+"""Parity of the HIP operator with the float64 oracle at the workloads' own per-call shapes.
+
+* Mixed-window stack (24 layers, B = 16, 12 q / 4 kv heads, head_dim 128, context 4096 + decode):
+  a producer call (window 1024, with the append), then the consumer calls that read its slot
+  (window -1 and 1024, no append), every row against the oracle.
+* Chunked prefill (B = 8, 32 q / 8 kv heads, 16384 tokens in chunks of 512): the last chunk,
+  positions 15872..16383 against a 15872-key prefix, where the cache offsets of the last row pass
+  200 MB; rows 0 and 7 against the oracle, the append of every row bit for bit.
+* Large-batch sampling decode (B = 64, 32 q / 8 kv heads, context U[2048, 2559]): one decode call
+  with the append, every row against the oracle.
+* The batched multi-prompt Decoder (ragged prompts, several samples each) against the same
+  Decoder on the CPU with the oracle operator: fp32 greedy ids identical and logits within 2e-4,
+  bf16 logits within bf16 tolerance.
+
+The oracle runs per row and per KV head (its query-head group), which keeps its float64 score
+matrices to a few hundred MB at these sizes.
+"""
+import numpy as np
+import pytest
+import torch
+
+from _util import ATOL, bits, max_abs, to_np
+from modelcore_amd.generate import sample_next_token
+from modelcore_amd.kernels.flash_attn import flash_attn
+from oracle import kv_oracle as ko
+from test_gpu_model import cpu_cache_copies, cpu_manager, gpu_manager, mixed_window_config  # noqa: F401
+from test_model_host import awake
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+CPU = torch.device("cpu")
+TOL = ATOL[torch.bfloat16]
+
+
+def _note(*a):
+    print("case:", *a, flush=True)
+
+
+def _draw(shape, g):
+    """N(0, 1) bf16 drawn on the GPU from a seeded generator (identical bytes reach the oracle
+    through the copy back)."""
+    return torch.randn(shape, generator=g, device=DEV).to(torch.bfloat16)
+
+
+def oracle_rows(q, k_cache, v_cache, k, v, seqlens, window, rows):
+    """float64 oracle output of the selected rows, (len(rows), T_new, H, D): the row's visible
+    prefix copied to the host, the new K/V appended, then one KV head (and its query heads) at a
+    time."""
+    outs = []
+    for b in rows:
+        L = int(seqlens[b])
+        T_new = q.shape[1]
+        qb = to_np(q[b:b + 1])
+        kb = to_np(k_cache[b:b + 1, :L + T_new])
+        vb = to_np(v_cache[b:b + 1, :L + T_new])
+        if k is not None:
+            kb[0, L:L + T_new] = to_np(k[b])
+            vb[0, L:L + T_new] = to_np(v[b])
+        H, H_kv = qb.shape[2], kb.shape[2]
+        G = H // H_kv
+        o = np.empty(qb.shape)
+        for j in range(H_kv):
+            o[:, :, j * G:(j + 1) * G] = ko.attention(qb[:, :, j * G:(j + 1) * G],
+                                                      kb[:, :, j:j + 1], vb[:, :, j:j + 1],
+                                                      [L], window)
+        outs.append(o)
+    return np.concatenate(outs)
+
+
+def _call(q, kc, vc, k, v, seqlens, window):
+    out = flash_attn.flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=seqlens,
+                                             causal=True, window_size=(window, 0))
+    torch.cuda.synchronize()
+    return out
+
+
+def test_mixed_window_stack_calls_at_b16_gqa12_4_context_4096():
+    B, H, H_kv, D, T_max, pos = 16, 12, 4, 128, 4352, 4096 + 200
+    g = torch.Generator(device=DEV).manual_seed(301)
+    kc, vc = _draw((B, T_max, H_kv, D), g), _draw((B, T_max, H_kv, D), g)
+    seqlens = torch.full((B,), pos, dtype=torch.int32, device=DEV)
+    k, v = _draw((B, 1, H_kv, D), g), _draw((B, 1, H_kv, D), g)
+    before = kc.clone()
+    _note("mixed: producer, window 1024, append")
+    q = _draw((B, 1, H, D), g)
+    out = _call(q, kc, vc, k, v, seqlens, 1024)
+    err = max_abs(to_np(out), oracle_rows(q, before, vc, k, v, seqlens, 1024, range(B)))
+    print(f"producer max-abs {err:.2e}", flush=True)
+    assert err <= TOL
+    assert torch.equal(kc[:, pos], k[:, 0]) and torch.equal(vc[:, pos], v[:, 0])
+    assert torch.equal(kc[:, :pos], before[:, :pos]) and torch.equal(kc[:, pos + 1:], before[:, pos + 1:])
+    for window in (-1, 1024):
+        _note("mixed: consumer, no append, window", window)
+        q = _draw((B, 1, H, D), g)
+        out = _call(q, kc, vc, None, None, seqlens, window)
+        err = max_abs(to_np(out), oracle_rows(q, kc, vc, None, None, seqlens, window, range(B)))
+        print(f"consumer window {window} max-abs {err:.2e}", flush=True)
+        assert err <= TOL
+
+
+def test_last_chunk_of_the_16k_chunked_prefill_at_gqa32_8():
+    B, H, H_kv, D, T_max, C = 8, 32, 8, 128, 16384, 512
+    pos = T_max - C
+    g = torch.Generator(device=DEV).manual_seed(302)
+    kc, vc = _draw((B, T_max, H_kv, D), g), _draw((B, T_max, H_kv, D), g)
+    q, k, v = _draw((B, C, H, D), g), _draw((B, C, H_kv, D), g), _draw((B, C, H_kv, D), g)
+    before_k, before_v = kc[[0, B - 1]].clone(), vc[[0, B - 1]].clone()
+    seqlens = torch.full((B,), pos, dtype=torch.int32, device=DEV)
+    _note("prefill last chunk: prefix", pos, "chunk", C)
+    out = _call(q, kc, vc, k, v, seqlens, -1)
+    assert torch.equal(kc[:, pos:], k) and torch.equal(vc[:, pos:], v)
+    want = oracle_rows(q[[0, B - 1]], before_k, before_v, k[[0, B - 1]], v[[0, B - 1]],
+                       seqlens[[0, B - 1]].cpu(), -1, range(2))
+    err = max_abs(to_np(out[[0, B - 1]]), want)
+    print(f"rows 0 and {B - 1}: max-abs {err:.2e}", flush=True)
+    assert err <= TOL
+
+
+def test_large_batch_sampling_decode_call_b64_gqa32_8():
+    B, H, H_kv, D, T_max = 64, 32, 8, 128, 2560
+    g = torch.Generator(device=DEV).manual_seed(303)
+    seqlens = torch.randint(2048, 2559 + 1, (B,), generator=torch.Generator().manual_seed(303),
+                            dtype=torch.int32)
+    kc, vc = _draw((B, T_max, H_kv, D), g), _draw((B, T_max, H_kv, D), g)
+    q, k, v = _draw((B, 1, H, D), g), _draw((B, 1, H_kv, D), g), _draw((B, 1, H_kv, D), g)
+    before = kc.clone()
+    _note("sampling decode call: B", B, "lengths", int(seqlens.min()), "..", int(seqlens.max()))
+    out = _call(q, kc, vc, k, v, seqlens.to(DEV), -1)
+    err = max_abs(to_np(out), oracle_rows(q, before, vc, k, v, seqlens, -1, range(B)))
+    print(f"max-abs {err:.2e}", flush=True)
+    assert err <= TOL
+    want_k = ko.append(bits(before), bits(before), bits(k), bits(k), seqlens.tolist())[0]
+    assert np.array_equal(bits(kc), want_k)
+
+
+def _decode(mgr, model, prompts, samples, n, feed=None):
+    """n greedy steps of the Decoder, or steps fed the columns of `feed` instead."""
+    dec = mgr.new_decoder(model, prompts, num_samples=samples, max_tokens=n)
+    logits, ids = [dec.logits.float().cpu()], []
+    for t in range(n):
+        nxt = sample_next_token(dec.logits, rng=None, temperature=0.0).view(-1) if feed is None \
+            else feed[:, t].to(dec.logits.device)
+        ids.append(nxt.cpu())
+        dec.step(nxt)
+        logits.append(dec.logits.float().cpu())
+    return torch.stack(ids, 1), logits, dec.kv_cache.cache_seqlens.cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_batched_multi_prompt_decoder_matches_the_cpu_oracle(dtype, cpu_cache_copies):  # noqa: F811
+    """The reference's multi-prompt flow (modelcore/generate.py:67-80 -> cache.py:92-119) is
+    one prefill and prefill_row per prompt; this build prefills the prompts together and places
+    each row at its own length. Both sides run this build's Decoder; the CPU one attends through
+    the oracle operator (whose Decoder equals per-prompt decoding, test_model_host.py). fp32:
+    the greedy ids are identical; bf16: fed the CPU's greedy ids, every step's logits stay within
+    bf16 tolerance."""
+    _note("multi-prompt decoder", dtype)
+    cfg = mixed_window_config(n_layer=4)
+    cpu_mgr = cpu_manager()
+    cpu_model = awake(cpu_mgr.create_model(cfg, device=CPU, seed=0))
+    gpu_mgr = gpu_manager(dtype)
+    gpu_model = gpu_mgr.create_model(cfg, device=DEV, seed=0)
+    gpu_model.load_state_dict(cpu_model.state_dict())
+    g = torch.Generator().manual_seed(7)
+    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist()
+               for n in (37, 150, 5, 88)]
+    with torch.no_grad():
+        want_ids, want_logits, want_len = _decode(cpu_mgr, cpu_model, prompts, 2, 8)
+        feed = None if dtype == torch.float32 else want_ids
+        got_ids, got_logits, got_len = _decode(gpu_mgr, gpu_model, prompts, 2, 8, feed)
+    assert torch.equal(got_len, want_len)
+    tol = 2e-4 if dtype == torch.float32 else 0.15
+    for i, (a, b) in enumerate(zip(got_logits, want_logits)):
+        err = (a - b).abs().max().item()
+        print(f"step {i}: logits max-abs {err:.2e} (scale {b.abs().max().item():.2f})", flush=True)
+        assert err <= tol, i
+    assert torch.equal(got_ids, want_ids)

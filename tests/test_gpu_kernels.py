@@ -182,8 +182,8 @@ def test_decode_matches_the_oracle(dtype, seqlens, H, H_kv, D, T_max, window):
 
 
 def test_repeated_decode_calls_are_deterministic():
-    """The split merge counts arrivals in the workspace and resets the counters: repeated calls,
-    also after a call of another shape on the same workspace, give identical bits."""
+    """The workspace is scratch shared by every call on the device: repeated calls, also after a
+    call of another shape that left its own partials in it, give identical bits."""
     c = make_case([700, 31, 2000, 256], 1, 16, 4, 128, 2100, torch.bfloat16, seed=23)
     first, _ = _run_op(c, -1)
     other = make_case([90, 1500], 1, 32, 8, 128, 1600, torch.bfloat16, seed=24)

@@ -270,3 +270,79 @@ def test_tiled_weights_round_trip_and_hold_64x128_blocks():
     assert torch.equal(untile_weight(t), w)
     with pytest.raises(ValueError):
         tile_weight(w[:100])
+
+
+def test_stepping_past_the_cache_raises_before_any_write():
+    """The reference fails at the cache write past T_max (modelcore/cache.py:105 for a prefill
+    row, an index error in the operator's append); the harness checks the room first, from the
+    host mirror, so the kernels never see such a step."""
+    mgr = manager()
+    model = mgr.create_model(tiny_config(), device=CPU, seed=0)
+    dec = mgr.new_decoder(model, [5, 17, 3], num_samples=2, max_tokens=2)
+    dec.step([1, 2])
+    dec.step([3, 4])
+    before = dec.kv_cache.k_cache.clone()
+    with pytest.raises(AssertionError, match="exceeds cache length"):
+        dec.step([5, 6])
+    assert torch.equal(dec.kv_cache.k_cache, before) and dec.kv_cache.get_pos() == 5
+    ragged = mgr.new_decoder(model, [[5, 17, 3], [9]], num_samples=1, max_tokens=1)
+    ragged.step([1, 2])
+    with pytest.raises(AssertionError, match="exceeds cache length"):
+        ragged.step([3, 4])
+
+
+def test_captured_step_refuses_layers_on_the_separate_rope_ops():
+    """A captured step replays whatever the capture recorded: the separate RoPE ops slice the
+    tables at the host position of that moment, so only layers on the fused step (positions
+    read on the device) may be captured."""
+    mgr = manager()  # the oracle operator: no fused pre-attention step
+    model = mgr.create_model(tiny_config(), device=CPU, seed=0)
+    dec = mgr.new_decoder(model, [5, 17, 3], num_samples=2, max_tokens=4)
+    with pytest.raises(ValueError, match="fused pre-attention"):
+        dec.capture(lambda logits, t: logits.argmax(-1))
+    for blk in model.body.blocks:
+        blk.mixer.epilogue = object()
+    model.set_fused_epilogue(False)
+    with pytest.raises(ValueError, match=r"layers \[0, 1, 2, 3\]"):
+        dec.capture(lambda logits, t: logits.argmax(-1))
+
+
+def test_linear_workspace_keeps_outgrown_buffers_alive(monkeypatch):
+    """A graph captured with the skinny GEMM's split-K workspace holds its address: when a larger
+    call replaces the buffer, the old one must stay allocated (not return to the allocator)."""
+    from modelcore_amd.kernels import linear as lin
+    monkeypatch.setattr(lin, "_WS", {})
+    monkeypatch.setattr(lin, "_RETIRED", [])
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    dev = torch.device("cpu", 0)
+    small = lin._workspace(dev, 1000)
+    assert lin._workspace(dev, 500) is small
+    big = lin._workspace(dev, small.numel() + 1)
+    assert big is not small and big.numel() >= 2 * small.numel()
+    assert any(t is small for t in lin._RETIRED)
+
+
+def test_checked_mode_raises_on_positions_past_the_cache(monkeypatch):
+    """Opt-in checked mode of the operator: positions read back on the host, IndexError before
+    any launch, as the reference's append raises (modelcore/kernels/flash_attn.py:336-346)."""
+    from modelcore_amd.kernels import flash_attn as fa
+    seen = []
+    monkeypatch.setattr(fa._ext, "require_rocm", lambda *a, **k: None)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    monkeypatch.setattr(fa._ext, "lib", lambda: seen.append("launch") or (_ for _ in ()).throw(
+        RuntimeError("no launch expected")))
+    fa.set_checked(True)
+    try:
+        q = torch.zeros(2, 1, 4, 16)
+        kc = torch.zeros(2, 8, 2, 16)
+        k = torch.zeros(2, 1, 2, 16)
+        with pytest.raises(IndexError, match="outside the cache of 8"):
+            fa.flash_attn_with_kvcache(q, kc, kc.clone(), k=k, v=k.clone(),
+                                       cache_seqlens=torch.tensor([3, 8], dtype=torch.int32))
+        with pytest.raises(IndexError):
+            fa.flash_attn_with_kvcache(q.expand(2, 2, 4, 16), kc, kc.clone(),
+                                       k=k.expand(2, 2, 2, 16), v=k.expand(2, 2, 2, 16),
+                                       cache_seqlens=torch.tensor([0, 7], dtype=torch.int32))
+        assert not seen
+    finally:
+        fa.set_checked(False)
