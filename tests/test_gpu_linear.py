@@ -98,3 +98,31 @@ def test_gated_silu_product_matches_the_separate_bf16_ops(m, hid, k, tiled):
     err = (h.float() - want).abs()
     assert torch.all(err <= want.abs() * 2.0 ** -7 + 1e-6), float(err.max())
     assert (h.float() == want.to(torch.bfloat16).float()).float().mean() > 0.99
+
+
+def test_a_captured_split_product_survives_a_larger_eager_call():
+    """A graph captured around a K-split product holds the workspace's address. An eager call
+    that needs a larger workspace replaces the buffer; the old one must stay allocated, so the
+    replays (with other eager work and allocations between them) still match the eager result."""
+    from modelcore_amd.kernels import linear as lin
+    g = torch.Generator().manual_seed(81)
+    x = torch.randn(16, 4096, generator=g).to(torch.bfloat16).to(DEV)
+    w = torch.randn(1024, 4096, generator=g).to(torch.bfloat16).to(DEV)
+    assert lin.k_splits(16, 1024, 4096) > 1
+    lin._RETIRED.extend(lin._WS.values())  # start from a workspace just large enough for this
+    lin._WS.clear()                         # product (earlier buffers stay alive)
+    eager = linear_bf16(x, w).clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = linear_bf16(x, w)
+    big_x = torch.randn(64, 8192, generator=g).to(torch.bfloat16).to(DEV)
+    big_w = torch.randn(4096, 8192, generator=g).to(torch.bfloat16).to(DEV)
+    old = lin._WS[DEV.index]
+    linear_bf16(big_x, big_w, splits=16)  # grows the workspace
+    assert lin._WS[DEV.index] is not old
+    for i in range(3):
+        junk = [torch.full((1 << 20,), 7.0, device=DEV) for _ in range(8)]  # reuse freed blocks
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), i
+        del junk
