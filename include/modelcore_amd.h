@@ -103,6 +103,25 @@ int mcamd_flash_attn_with_kvcache(const void *q, const void *k, const void *v,
                                   void *stream);
 
 /*
+ * mcamd_flash_attn_with_kvcache without the workspace arguments, for callers that cannot allocate
+ * device memory (code under graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * It has no counterpart in the reference. Its scratch is a static device array of
+ * MCAMD_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends), shared by every call on that
+ * GPU: calls that overlap on one GPU race. Sizes whose decode partials need more scratch than that
+ * (mcamd_attn_workspace_bytes() > MCAMD_NOALLOC_SCRATCH_BYTES) return MCAMD_EWORKSPACE. The
+ * stream's device must be the current device. Otherwise identical to
+ * mcamd_flash_attn_with_kvcache, with the same kernels and bit-identical results.
+ */
+#define MCAMD_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int mcamd_flash_attn_with_kvcache_noalloc(const void *q, const void *k, const void *v,
+                                          void *k_cache, void *v_cache,
+                                          const int32_t *cache_seqlens, void *out, int64_t batch,
+                                          int64_t t_new, int64_t n_head, int64_t n_kv_head,
+                                          int64_t head_dim, int64_t t_max,
+                                          int64_t cache_batch_stride, int64_t window, int causal,
+                                          int dtype, void *stream);
+
+/*
  * Attention only (no append), one query token per row: the decode half of
  * mcamd_flash_attn_with_kvcache for t_new == 1 (modelcore/kernels/flash_attn.py:348-366 with
  * T_new == 1). Exposed separately so the append and the attention can be timed apart.

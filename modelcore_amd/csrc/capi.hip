@@ -35,7 +35,7 @@ int check_attn_shapes(const AttnArgs &a, bool need_workspace) {
   if (need_workspace) {
     const size_t need =
         decode_workspace_bytes(a.batch, a.n_head, a.n_kv_head, a.head_dim, a.t_max, a.window);
-    if (!a.workspace || a.workspace_bytes < need)
+    if (need > 0 && (!a.workspace || a.workspace_bytes < need))
       return fail(MCAMD_EWORKSPACE, "attention: workspace smaller than mcamd_attn_workspace_bytes() (" +
                                         std::to_string(need) + " bytes)");
     if (!aligned(a.workspace, 16)) return fail(MCAMD_EINVAL, "attention: workspace not 16-byte aligned");
@@ -47,7 +47,7 @@ int check_attn_shapes(const AttnArgs &a, bool need_workspace) {
 
 using namespace mcamd;
 
-extern "C" int mcamd_abi_version(void) { return 4; }
+extern "C" int mcamd_abi_version(void) { return 5; }
 
 extern "C" const char *mcamd_last_error(void) { return g_last_error.c_str(); }
 
