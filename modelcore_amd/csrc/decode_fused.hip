@@ -64,15 +64,30 @@ constexpr int kMinKeysPerGroup = MCAMD_DECODE_MIN_KEYS;  // fewer workgroups whe
 #define MCAMD_DECODE_RING 2
 #endif
 constexpr int kRing = MCAMD_DECODE_RING;  // tile buffers per wave (kRing - 1 tiles in flight)
+#ifndef MCAMD_DECODE_WAVES
+#define MCAMD_DECODE_WAVES 4
+#endif
+constexpr int NW = MCAMD_DECODE_WAVES;  // waves per workgroup: 4 (one per SIMD) or 8 (two)
+static_assert(NW == 4 || NW == 8, "the four-row merge at a segment end takes 4 or 8 waves");
+constexpr int kMergeSplit = NW / 4;          // waves per KV-head row in that merge
+constexpr int kMergeDims = 128 / 16 / kMergeSplit;  // dims per lane in that merge (8 or 4)
 #ifndef MCAMD_DECODE_SEG_COST
 #define MCAMD_DECODE_SEG_COST 96
 #endif
 constexpr int kSegCost = MCAMD_DECODE_SEG_COST;  // key-free lead slots per unit (see unit_span)
 constexpr int kPart = KG * GM * D + 2 * KG * GM;  // floats per partial: o[16][D], (m, l)[16]
-// Segments whose loads the merge keeps in flight: 8, or 16 when the split gives a unit more than
-// 8 workgroups on average (short windowed calls: on a 24-layer mixed-window stack, 0.435 ms per
-// step against 0.438 with 8).
-constexpr int kMergeBatch = 8, kMergeBatchWide = 16;
+#ifndef MCAMD_DECODE_BUCKET
+#define MCAMD_DECODE_BUCKET 16
+#endif
+// Partial slots per unit at addresses fixed by the unit alone (segment j of unit u in slot
+// u * kBucket + j), so that the merge pass loads them in the same round trip as the unit's
+// segment count; segments past kBucket go to an overflow area found through the descriptor.
+constexpr int kBucket = MCAMD_DECODE_BUCKET;
+#ifndef MCAMD_DECODE_SPEC
+#define MCAMD_DECODE_SPEC 16
+#endif
+constexpr int kSpec = MCAMD_DECODE_SPEC;  // bucket slots the merge loads before the count is known
+static_assert(kSpec <= kBucket, "speculative merge loads stay inside the unit's bucket");
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -82,7 +97,8 @@ struct FusedParams {
   uint16_t *k_cache, *v_cache;
   const int32_t *seqlens;
   uint16_t *out;
-  float *part;  // [n_groups + B * n_units][kPart]: segment partials, slot = group + unit
+  float *part;  // [B * n_units * kBucket][kPart]: segment j < kBucket of unit u at u * kBucket + j
+  float *over;  // [kMaxGroups + B * n_units][kPart]: segments j >= kBucket, slot = group + unit
   int2 *desc;   // [B * n_units]: (first workgroup, segments) of each unit that has keys
   int B, H, H_kv, G, n_hc, n_kg, n_units, T_max, window, n_groups;
   int scan32;  // B <= 64 and every sum of row slot counts fits in 31 bits
@@ -289,8 +305,8 @@ __device__ void locate(const FusedParams &P, int g, int lane, int64_t &T, int &N
   find_row(P, start, lane, b, Pb);
 }
 
-__global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
-  __shared__ WaveAcc s_acc[4];
+__global__ __launch_bounds__(64 * NW) void decode_fused_kernel(FusedParams P) {
+  __shared__ WaveAcc s_acc[NW];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;  // wave within the workgroup
   const int g = blockIdx.x;
@@ -301,7 +317,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
   for (int b = g; b < P.B; b += P.n_groups) {
     int lo;
     if (row_keys(P, b, lo) == 0)
-      for (int i = threadIdx.x; i < P.H * D; i += 256) P.out[int64_t(b) * P.H * D + i] = 0x7fc0;
+      for (int i = threadIdx.x; i < P.H * D; i += 64 * NW) P.out[int64_t(b) * P.H * D + i] = 0x7fc0;
   }
   // NG <= T active workgroups: every range [g*T/NG, (g+1)*T/NG) is then non-empty, so the
   // workgroups holding a unit's keys are exactly those from its first key's owner to its last
@@ -454,19 +470,19 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
       }
     };
 
-    // The workgroup's four waves share the segment: wave wv takes tiles wv, wv + 4, ... . A ring
-    // of kRing tile buffers keeps kRing - 1 tiles' loads in flight while one is consumed (with
-    // one wave per SIMD, this prefetch depth is what hides the memory latency).
+    // The workgroup's NW waves share the segment: wave wv takes tiles wv, wv + NW, ... . A ring
+    // of kRing tile buffers keeps kRing - 1 tiles' loads in flight while one is consumed (this
+    // prefetch depth, times the waves per SIMD, is what hides the memory latency).
     const int ntile = (seg + kTokens - 1) / kTokens;
     Tile ring[kRing];
 #pragma unroll
-    for (int i = 0; i < kRing - 1; ++i) load_tile(ring[i], wv + 4 * i);
-    for (int tile = wv; tile < ntile; tile += 4 * kRing) {
+    for (int i = 0; i < kRing - 1; ++i) load_tile(ring[i], wv + NW * i);
+    for (int tile = wv; tile < ntile; tile += NW * kRing) {
 #pragma unroll
       for (int u = 0; u < kRing; ++u) {
-        const int cur = tile + 4 * u;
+        const int cur = tile + NW * u;
         if (cur >= ntile) break;
-        load_tile(ring[(u + kRing - 1) % kRing], cur + 4 * (kRing - 1));
+        load_tile(ring[(u + kRing - 1) % kRing], cur + NW * (kRing - 1));
         process(ring[u], cur);
       }
     }
@@ -488,44 +504,44 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
     lds_barrier();  // not __syncthreads(): its global fence would wait for the prefetch past
                     // the segment; the waves share nothing through global memory
 
-    // Merge the four waves: wave wv now owns KV-head row wv; lane (h, c) = (lane / 16, lane % 16)
-    // owns head h and dims c*8..c*8+7 of that row.
-    const int mr = wv;
+    // Merge the waves: wave wv now owns KV-head row wv % 4 and, with eight waves, half of its
+    // dims; lane (h, c) = (lane / 16, lane % 16) owns head h and kMergeDims dims from d0.
+    const int mr = wv % KG;
     const int mh = lane >> 4;
+    const int d0 = (wv / KG) * (D / kMergeSplit) + c * kMergeDims;
     float M = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) M = fmaxf(M, s_acc[u].m[mr][mh]);
-    float L = 0.f, acc[8];
+    for (int u = 0; u < NW; ++u) M = fmaxf(M, s_acc[u].m[mr][mh]);
+    float L = 0.f, acc[kMergeDims];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+    for (int e = 0; e < kMergeDims; ++e) acc[e] = 0.f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NW; ++u) {
       const float wgt = exp2_or_zero(s_acc[u].m[mr][mh] - M);
       L += s_acc[u].l[mr][mh] * wgt;
-      const float4 a = *reinterpret_cast<const float4 *>(&s_acc[u].o[mr][mh][c * 8]);
-      const float4 bq = *reinterpret_cast<const float4 *>(&s_acc[u].o[mr][mh][c * 8 + 4]);
-      acc[0] = fmaf(a.x, wgt, acc[0]);
-      acc[1] = fmaf(a.y, wgt, acc[1]);
-      acc[2] = fmaf(a.z, wgt, acc[2]);
-      acc[3] = fmaf(a.w, wgt, acc[3]);
-      acc[4] = fmaf(bq.x, wgt, acc[4]);
-      acc[5] = fmaf(bq.y, wgt, acc[5]);
-      acc[6] = fmaf(bq.z, wgt, acc[6]);
-      acc[7] = fmaf(bq.w, wgt, acc[7]);
+#pragma unroll
+      for (int e4 = 0; e4 < kMergeDims; e4 += 4) {
+        const float4 a = *reinterpret_cast<const float4 *>(&s_acc[u].o[mr][mh][d0 + e4]);
+        acc[e4 + 0] = fmaf(a.x, wgt, acc[e4 + 0]);
+        acc[e4 + 1] = fmaf(a.y, wgt, acc[e4 + 1]);
+        acc[e4 + 2] = fmaf(a.z, wgt, acc[e4 + 2]);
+        acc[e4 + 3] = fmaf(a.w, wgt, acc[e4 + 3]);
+      }
     }
 
     // This row's output heads (a row past H_kv writes nothing).
     const int m_kvh = kg * KG + mr;
     const bool m_live = m_kvh < P.H_kv && mh < min(GM, P.G - hc * GM);
-    uint16_t *out_at = P.out + (int64_t(b) * P.H + int64_t(m_kvh) * P.G + hc * GM + mh) * D + c * 8;
-    auto write_out = [&](const float (&v)[8], float denom) {
+    uint16_t *out_at = P.out + (int64_t(b) * P.H + int64_t(m_kvh) * P.G + hc * GM + mh) * D + d0;
+    auto write_out = [&](const float (&v)[kMergeDims], float denom) {
       const float inv = 1.f / denom;
-      uint4 v4;
-      v4.x = pack_bf16(v[0] * inv, v[1] * inv);
-      v4.y = pack_bf16(v[2] * inv, v[3] * inv);
-      v4.z = pack_bf16(v[4] * inv, v[5] * inv);
-      v4.w = pack_bf16(v[6] * inv, v[7] * inv);
-      *reinterpret_cast<uint4 *>(out_at) = v4;
+      uint32_t w[kMergeDims / 2];
+#pragma unroll
+      for (int e = 0; e < kMergeDims / 2; ++e) w[e] = pack_bf16(v[2 * e] * inv, v[2 * e + 1] * inv);
+      if constexpr (kMergeDims == 8)
+        *reinterpret_cast<uint4 *>(out_at) = make_uint4(w[0], w[1], w[2], w[3]);
+      else
+        *reinterpret_cast<uint2 *>(out_at) = make_uint2(w[0], w[1]);
     };
 
     // The ring's registers stay allocated to it up to here, after the four-wave merge: the
@@ -544,13 +560,19 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
     if (g_first == g_last) {
       if (m_live) write_out(acc, L);  // the segment is the whole unit
     } else {
-      // This workgroup's partial for the unit: slot g + ug, distinct for every segment. The
-      // merge kernel, launched next on the same stream, combines a unit's partials.
-      float *slot = P.part + int64_t(g + ug) * kPart;
-      float *po = slot + (mr * GM + mh) * D + c * 8;
-      *reinterpret_cast<float4 *>(po) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-      *reinterpret_cast<float4 *>(po + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
-      if (c == 0) *reinterpret_cast<float2 *>(slot + KG * GM * D + 2 * (mr * GM + mh)) = make_float2(M, L);
+      // This workgroup's partial for the unit, segment j = g - g_first: bucket slot j of the
+      // unit, or overflow slot g + ug (distinct for every segment: the next unit's first
+      // workgroup is at least this unit's last). The merge kernel, launched next on the same
+      // stream, combines a unit's partials.
+      const int j = g - g_first;
+      float *slot = j < kBucket ? P.part + (int64_t(ug) * kBucket + j) * kPart
+                                : P.over + int64_t(g + ug) * kPart;
+      float *po = slot + (mr * GM + mh) * D + d0;
+#pragma unroll
+      for (int e4 = 0; e4 < kMergeDims; e4 += 4)
+        *reinterpret_cast<float4 *>(po + e4) = make_float4(acc[e4], acc[e4 + 1], acc[e4 + 2], acc[e4 + 3]);
+      if (c == 0 && wv < KG)
+        *reinterpret_cast<float2 *>(slot + KG * GM * D + 2 * (mr * GM + mh)) = make_float2(M, L);
     }
     lds_barrier();  // s_acc is reused by the next segment
 
@@ -567,9 +589,13 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedParams P) {
 }
 
 // Merge pass with one wave per (unit, query head): lane l combines dims 2l, 2l+1 of that head
-// over the unit's segments, BATCH segments' loads in flight at a time.
-template <int BATCH>
+// over the unit's segments. The loads of the unit's first SPEC bucket slots are issued with those
+// of its descriptor and row length, before the segment count is known (one memory round trip for
+// units of up to SPEC segments; slots past the count hold other calls' data and are ignored);
+// later segments follow BATCH at a time.
+template <int SPEC>
 __global__ __launch_bounds__(64) void decode_merge_kernel(FusedParams P) {
+  constexpr int BATCH = 8;
   const int lane = threadIdx.x;
   const int ug = blockIdx.x / (KG * GM);
   const int hr = blockIdx.x - ug * (KG * GM);  // KV row * GM + head within the unit
@@ -580,33 +606,47 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(FusedParams P) {
   const int kvh = kg * KG + hr / GM;
   const int hh = hr % GM;
   if (kvh >= P.H_kv || hh >= min(GM, P.G - hc * GM)) return;
-  // The unit's (first workgroup, segments), published by the streaming pass; a row outside
-  // the cache has no keys and no descriptor (its NaN output is written), so it is checked too.
-  int lo;
+  const float *bucket = P.part + int64_t(ug) * kBucket * kPart;
+  auto seg_at = [&](int j, int g_first) {
+    return j < kBucket ? bucket + int64_t(j) * kPart : P.over + int64_t(g_first + j + ug) * kPart;
+  };
+  // The unit's (first workgroup, segments), published by the streaming pass; a row outside the
+  // cache has no keys and no descriptor (its NaN output is written), so it is checked too.
   const int2 d = P.desc[ug];
-  if (row_keys(P, b, lo) == 0) return;
+  int lo;
+  const int nk = row_keys(P, b, lo);
+  float2 ml[SPEC], v[SPEC];
+#pragma unroll
+  for (int k = 0; k < SPEC; ++k) {
+    const float *ps = bucket + int64_t(k) * kPart;
+    ml[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * hr);
+    v[k] = *reinterpret_cast<const float2 *>(ps + hr * D + 2 * lane);
+  }
+  if (nk == 0) return;
   const int g_first = d.x, nseg = d.y;
   if (nseg == 1) return;  // written directly by the streaming pass
-  const float *base = P.part + int64_t(g_first + ug) * kPart;
   float M = -INFINITY, L = 0.f, t0 = 0.f, t1 = 0.f;
-  for (int s0 = 0; s0 < nseg; s0 += BATCH) {
-    float2 ml[BATCH], v[BATCH];
+  auto add = [&](float2 mlk, float2 vk, bool valid) {
+    const float mk = valid ? mlk.x : -INFINITY;
+    const float m_new = fmaxf(M, mk);
+    const float fa = exp2_or_zero(M - m_new), fb = exp2_or_zero(mk - m_new);
+    L = L * fa + (valid ? mlk.y : 0.f) * fb;
+    t0 = t0 * fa + (valid ? vk.x : 0.f) * fb;
+    t1 = t1 * fa + (valid ? vk.y : 0.f) * fb;
+    M = m_new;
+  };
+#pragma unroll
+  for (int k = 0; k < SPEC; ++k) add(ml[k], v[k], k < nseg);
+  for (int s0 = SPEC; s0 < nseg; s0 += BATCH) {
+    float2 mb[BATCH], vb[BATCH];
 #pragma unroll
     for (int k = 0; k < BATCH; ++k) {
-      const float *ps = base + int64_t(min(s0 + k, nseg - 1)) * kPart;
-      ml[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * hr);
-      v[k] = *reinterpret_cast<const float2 *>(ps + hr * D + 2 * lane);
+      const float *ps = seg_at(min(s0 + k, nseg - 1), g_first);
+      mb[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * hr);
+      vb[k] = *reinterpret_cast<const float2 *>(ps + hr * D + 2 * lane);
     }
 #pragma unroll
-    for (int k = 0; k < BATCH; ++k) {
-      const float mk = s0 + k < nseg ? ml[k].x : -INFINITY;
-      const float m_new = fmaxf(M, mk);
-      const float fa = exp2_or_zero(M - m_new), fb = exp2_or_zero(mk - m_new);
-      L = L * fa + ml[k].y * fb;
-      t0 = t0 * fa + v[k].x * fb;
-      t1 = t1 * fa + v[k].y * fb;
-      M = m_new;
-    }
+    for (int k = 0; k < BATCH; ++k) add(mb[k], vb[k], s0 + k < nseg);
   }
   const float inv = 1.f / L;
   *reinterpret_cast<uint32_t *>(P.out + (int64_t(b) * P.H + int64_t(kvh) * P.G + hc * GM + hh) * D +
@@ -639,7 +679,7 @@ size_t decode_fused_partial_bytes(int64_t batch, int64_t n_head, int64_t n_kv_he
   (void)t_max;
   (void)window;
   const int64_t units = batch * decode_fused_units(n_head, n_kv_head);
-  return size_t((kMaxGroups + units) * kPart * 4 + units * int64_t(sizeof(int2)));
+  return size_t((units * kBucket + kMaxGroups + units) * kPart * 4 + units * int64_t(sizeof(int2)));
 }
 
 bool decode_fused_supported(const AttnArgs &a) {
@@ -678,16 +718,15 @@ int launch_decode_fused(const AttnArgs &a) {
   groups = std::max<int64_t>(1, std::min<int64_t>(groups, (t_upper + kMinKeysPerGroup - 1) / kMinKeysPerGroup));
   P.n_groups = int(groups);
   char *ws = static_cast<char *>(a.workspace);
+  const int64_t units = int64_t(P.B) * P.n_units;
   P.part = reinterpret_cast<float *>(ws);
-  P.desc = reinterpret_cast<int2 *>(P.part + (kMaxGroups + int64_t(P.B) * P.n_units) * kPart);
-  hipLaunchKernelGGL(decode_fused_kernel, dim3(unsigned(groups)), dim3(256), 0, a.stream, P);
+  P.over = P.part + units * kBucket * kPart;
+  P.desc = reinterpret_cast<int2 *>(P.over + (kMaxGroups + units) * kPart);
+  hipLaunchKernelGGL(decode_fused_kernel, dim3(unsigned(groups)), dim3(64 * NW), 0, a.stream, P);
   int st = launch_status("decode_fused");
   if (st != MCAMD_OK) return st;
   const dim3 merge_grid(unsigned(a.batch * P.n_units * KG * GM));
-  if (groups > int64_t(kMergeBatch) * a.batch * P.n_units)
-    hipLaunchKernelGGL(decode_merge_kernel<kMergeBatchWide>, merge_grid, dim3(64), 0, a.stream, P);
-  else
-    hipLaunchKernelGGL(decode_merge_kernel<kMergeBatch>, merge_grid, dim3(64), 0, a.stream, P);
+  hipLaunchKernelGGL(decode_merge_kernel<kSpec>, merge_grid, dim3(64), 0, a.stream, P);
   return launch_status("decode_merge");
 }
 

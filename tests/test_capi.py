@@ -56,9 +56,10 @@ def test_workspace_size_follows_the_split_count():
     B, H, D, T_max = 32, 16, 128, 8300
     n_splits = -(-T_max // 256)
     general = B * H * n_splits * (D + 2) * 4  # per-(row, head, split) partials, general kernel
-    # per-segment partials (16 heads), bf16 / D=128, then one (first group, segments) int pair
-    # per unit (H = 16 query heads over 4 KV heads: one unit per row)
-    fused = (1024 + B) * (16 * (D + 2)) * 4 + B * 8
+    # per-segment partials (16 heads), bf16 / D=128: a bucket of 16 slots per unit, an overflow
+    # area of 1024 + units slots, then one (first group, segments) int pair per unit
+    # (H = 16 query heads over 4 KV heads: one unit per row)
+    fused = (16 * B + 1024 + B) * (16 * (D + 2)) * 4 + B * 8
     got = lib.mcamd_attn_workspace_bytes(B, 1, H, 4, D, T_max, -1)
     assert max(general, fused) <= got < max(general, fused) + 256  # scratch only, no counters
     windowed = lib.mcamd_attn_workspace_bytes(B, 1, H, 4, D, T_max, 1024)
