@@ -12,6 +12,14 @@ Prints one JSON line: tokens/s (32 tokens per step), the roofline of the decode 
 fallback timed on this host's cores on the same workload.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline]
+
+The roofline figure times the decode call alone, ROOF_LAUNCHES launches at the drawn lengths
+(seed 0), whatever --steps and --warmup are, so that its bytes -- and the HBM traffic the
+committed counter profile measured for the same launches -- do not depend on them. Two modes
+turn rocprofv3 output into the committed summaries (no GPU needed):
+
+    python bench.py --summarize-traffic FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
+    python bench.py --summarize-trace KERNEL_TRACE.csv [--launches N]
 """
 from __future__ import annotations
 
@@ -25,9 +33,25 @@ import time
 METRIC = "decode tok/s at B=32 ctx 8k GQA16/4 hd128; KV path HBM GB/s as % of peak"
 B, H, H_KV, D = 32, 16, 4, 128
 L_MIN, L_MAX = 512, 8192
-HBM_PEAK = 8.0e12
 COPY_BYTES = 1 << 30
 TRAFFIC_FILE = "profiles/decode_b32_gqa16x4_hd128_ctx8k_traffic.md"
+ROOF_LAUNCHES = 200  # decode calls in the roofline loop
+DECODE_KERNELS = ("decode_fused_kernel", "decode_merge_kernel")
+
+
+def peaks():
+    """(HBM bytes/s, dense bf16 FLOP/s, how they were found) of GPU 0: the reference's MI355
+    denominators (modelcore/runtime.py:162, :200), found by device name or gfx950 architecture."""
+    from modelcore_amd import runtime
+    bw, fl, how = runtime.device_peaks(0)
+    if bw == float("inf"):
+        raise RuntimeError(f"no peak figures for this GPU ({how}): the roofline needs them")
+    return bw, fl, how
+
+
+def host_cores():
+    """Every core this process may run on (the CPU baseline's thread count, reported with it)."""
+    return len(os.sched_getaffinity(0))
 
 
 def log(msg):
@@ -60,20 +84,118 @@ def parse_args():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain device copy of COPY_BYTES, ten times (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--summarize-traffic", nargs=4, metavar="CSV",
+                    help="print the traffic summary of the decode call from rocprofv3 --pmc "
+                         "FETCH_SIZE and WRITE_SIZE runs of `bench.py --eager --no-cpu-baseline` and "
+                         "of `bench.py --calibrate-copy` (counter_collection.csv files)")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="print the mean duration of the decode call's kernels over the last "
+                         "--launches dispatches of a rocprofv3 kernel_trace.csv")
+    ap.add_argument("--launches", type=int, default=ROOF_LAUNCHES)
     return ap.parse_args()
 
 
-def measured_traffic():
-    """HBM bytes per launch of the decode call, as the rocprofv3 FETCH_SIZE and WRITE_SIZE runs
-    recorded them (scaled by the copy calibration) in the committed profile summary, or None."""
+def drawn_lengths(seed=0):
+    """The decode microbench's per-row cache lengths: U[512, 8192], drawn first from the seeded
+    CPU generator (the bench draws its caches and tokens from the same generator after them)."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(L_MIN, L_MAX + 1, (B,), generator=g, dtype=torch.int32)
+
+
+def roofline_bytes(seed=0):
+    """Algorithmic bytes of one decode call of the roofline loop (append + attention of every row
+    at its drawn length)."""
+    from modelcore_amd import stats
+    return stats.decode_step_bytes(drawn_lengths(seed).tolist(), H, H_KV, D, 2, append=True)
+
+
+def measured_traffic(bytes_now):
+    """(HBM bytes per launch of the decode call, where the figure comes from) from the committed
+    counter profile: its own figure when it was measured for launches of these algorithmic bytes,
+    else its traffic/bytes ratio applied to these bytes (said so); (None, reason) without one."""
     import re
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_FILE)
     try:
         with open(path) as f:
-            m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
+            text = f.read()
     except OSError:
-        return None
-    return int(m.group(1)) if m else None
+        return None, f"{TRAFFIC_FILE} missing"
+    t = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
+    a = re.search(r"^algorithmic_bytes_per_launch:\s*(\d+)", text, re.M)
+    if not (t and a):
+        return None, f"{TRAFFIC_FILE} holds no per-launch figures"
+    traffic, algo = int(t.group(1)), int(a.group(1))
+    how = (f"{TRAFFIC_FILE}: rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE (copy-calibrated), mean over the "
+           f"{ROOF_LAUNCHES} launches of this loop")
+    if algo == bytes_now:
+        return traffic, how + ", same positions"
+    return round(traffic / algo * bytes_now), how + (f", measured at {algo} algorithmic bytes and "
+                                                     f"scaled by its ratio {traffic / algo:.4f}")
+
+
+def _counter_rows(path):
+    import csv
+    with open(path) as f:
+        return list(csv.DictReader(f))
+
+
+def summarize_traffic(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv):
+    """Markdown summary of the decode call's HBM traffic (the roofline loop's launches)."""
+    import statistics as st
+
+    def per_kernel(rows, counter, names, last):
+        out = {}
+        for name in names:
+            vals = [float(r["Counter_Value"]) for r in rows
+                    if r["Counter_Name"] == counter and name in r["Kernel_Name"]]
+            out[name] = vals[-last:]
+        return out
+
+    def copy_scale(rows, counter):
+        vals = [float(r["Counter_Value"]) for r in rows
+                if r["Counter_Name"] == counter and "copyBuffer" in r["Kernel_Name"]]
+        kib = st.median(vals)
+        return kib, COPY_BYTES / 1024 / kib
+
+    cf_kib, cf_scale = copy_scale(_counter_rows(copy_fetch_csv), "FETCH_SIZE")
+    cw_kib, cw_scale = copy_scale(_counter_rows(copy_write_csv), "WRITE_SIZE")
+    fetch = per_kernel(_counter_rows(fetch_csv), "FETCH_SIZE", DECODE_KERNELS, ROOF_LAUNCHES)
+    write = per_kernel(_counter_rows(write_csv), "WRITE_SIZE", DECODE_KERNELS, ROOF_LAUNCHES)
+    algo = roofline_bytes()
+    lines = ["| kernel | launches | FETCH_SIZE (KiB, mean) | x scale | WRITE_SIZE (KiB, mean) | x scale |",
+             "|---|---|---|---|---|---|"]
+    total = 0.0
+    for name in DECODE_KERNELS:
+        fk, wk = st.mean(fetch[name]), st.mean(write[name])
+        total += fk * cf_scale * 1024 + wk * cw_scale * 1024
+        lines.append(f"| {name} | {len(fetch[name])} | {fk:.2f} | {fk * cf_scale:.2f} | {wk:.2f} | "
+                     f"{wk * cw_scale:.2f} |")
+    print(f"Calibration (plain device copy of {COPY_BYTES >> 20} MiB, `__amd_rocclr_copyBuffer`): "
+          f"FETCH_SIZE reads {cf_kib:.1f} KiB per launch (scale {cf_scale:.3f}), WRITE_SIZE "
+          f"{cw_kib:.1f} KiB (scale {cw_scale:.3f}).\n")
+    print("\n".join(lines))
+    print(f"\nPer launch of the decode call: {round(total)} bytes of HBM traffic against {algo} "
+          f"algorithmic bytes: {total / algo:.3f}x.\n")
+    print(f"traffic_bytes_per_launch: {round(total)}")
+    print(f"algorithmic_bytes_per_launch: {algo}")
+
+
+def summarize_trace(trace_csv, launches):
+    """Mean durations (us) of the decode call's kernels over their last `launches` dispatches."""
+    import statistics as st
+    rows = _counter_rows(trace_csv)
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    total = 0.0
+    for name in DECODE_KERNELS:
+        d = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows
+             if name in r["Kernel_Name"]][-launches:]
+        total += st.mean(d)
+        print(f"| {name} | {len(d)} | {st.mean(d):.2f} | {st.median(d):.2f} | {min(d):.2f} | "
+              f"{max(d):.2f} |")
+    algo = roofline_bytes()
+    print(f"\nsum of means: {total:.2f} us per call; {algo} algorithmic bytes -> "
+          f"{algo / total / 1e3:.1f} GB/s")
 
 
 def calibrate_copy():
@@ -91,7 +213,6 @@ def calibrate_copy():
 
 
 PF_B, PF_T, PF_C, PF_H, PF_HKV = 8, 16384, 512, 32, 8
-MFMA_BF16_PEAK = 2.5e15
 
 
 def bench_prefill(args):
@@ -162,6 +283,7 @@ def bench_prefill(args):
     attn_ms = start.elapsed_time(end) / K
     flops = sum(stats.prefill_flops([c * PF_C] * PF_B, PF_C, PF_H, D) for c in range(n_chunks))
     achieved = flops / (attn_ms * 1e-3)
+    _, flops_peak, peak_src = peaks()
     result = {
         "metric": "chunked prefill tok/s at B=8, 16384 tokens in chunks of 512, GQA 32/8 hd128; "
                   "attention MFMA utilisation",
@@ -175,8 +297,9 @@ def bench_prefill(args):
                    "batch": PF_B, "tokens": PF_T, "chunk": PF_C, "n_head": PF_H,
                    "n_kv_head": PF_HKV, "head_dim": D},
         "roofline": {"kernel": "prefill_mfma_kernel (attention of the 32 chunks)", "bound": "mfma",
-                     "achieved": round(achieved / 1e12, 1), "peak": MFMA_BF16_PEAK / 1e12,
-                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK, 4),
+                     "achieved": round(achieved / 1e12, 1), "peak": flops_peak / 1e12,
+                     "peak_source": peak_src,
+                     "unit": "TFLOP/s", "frac": round(achieved / flops_peak, 4),
                      "traffic": None, "ms_per_pass": round(attn_ms, 4), "flops_per_pass": flops},
     }
     if not args.no_cpu_baseline:
@@ -190,7 +313,7 @@ def cpu_prefill_baseline(q, k, v, budget_s=15.0):
     import torch
     from oracle import sdpa_fallback
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = host_cores()
     torch.set_num_threads(cores)
     a = PF_T // 2
     end = a + PF_C
@@ -250,6 +373,7 @@ def bench_replicate(args):
     ms = start.elapsed_time(end) / K
     nbytes = stats.replicate_bytes(RP_SLOTS, RP_ROWS, RP_P, RP_HKV, D, 2)
     gbps = nbytes / (ms * 1e-3) / 1e9
+    hbm_peak, _, peak_src = peaks()
     result = {
         "metric": "KV replication GB/s: 2048-token prompt cache, 32 layers x 8 kv heads x hd128, "
                   "into 64 rows; % of HBM peak",
@@ -261,7 +385,8 @@ def bench_replicate(args):
                    "slots": RP_SLOTS, "prompt": RP_P, "rows": RP_ROWS, "n_kv_head": RP_HKV,
                    "head_dim": D},
         "roofline": {"kernel": "kv_replicate_kernel", "bound": "hbm", "achieved": round(gbps, 1),
-                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(gbps * 1e9 / HBM_PEAK, 4),
+                     "peak": hbm_peak / 1e9, "peak_source": peak_src, "unit": "GB/s",
+                     "frac": round(gbps * 1e9 / hbm_peak, 4),
                      "traffic": None, "bytes_per_launch": nbytes},
     }
     if not args.no_cpu_baseline:
@@ -276,7 +401,7 @@ def cpu_replicate_baseline(src, budget_s=10.0):
     from modelcore_amd import stats
     from oracle import sdpa_fallback
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = host_cores()
     torch.set_num_threads(cores)
     n_slots = 2
     sk, sv = src.k_cache[:n_slots].cpu(), src.v_cache[:n_slots].cpu()
@@ -354,7 +479,8 @@ def bench_mixed(args):
             total += stats.decode_step_bytes(pos, MX_H, MX_HKV, D, 2, window=w)
     step_bytes = total / K
     gbps = step_bytes / (ms * 1e-3) / 1e9
-    print(json.dumps({
+    hbm_peak, _, peak_src = peaks()
+    result = {
         "metric": "mixed-window stack decode: KV-path GB/s per step, 24 layers (3:1 local 1024 / "
                   "global), KV sharing, B=16, ctx 4096, GQA 12/4 hd128",
         "value": round(MX_B / (ms * 1e-3), 1), "unit": "tok/s", "n_gpus": 1, "steps": K,
@@ -365,14 +491,119 @@ def bench_mixed(args):
                                "positions 4096+", "layers": MX_LAYERS, "batch": MX_B,
                    "n_head": MX_H, "n_kv_head": MX_HKV, "head_dim": D, "timing": "hip_graph"},
         "roofline": {"kernel": "decode_fused_kernel + decode_merge_kernel (24 calls per step)",
-                     "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": round(gbps * 1e9 / HBM_PEAK, 4), "traffic": None,
+                     "bound": "hbm", "achieved": round(gbps, 1), "peak": hbm_peak / 1e9,
+                     "peak_source": peak_src, "unit": "GB/s",
+                     "frac": round(gbps * 1e9 / hbm_peak, 4), "traffic": None,
                      "bytes_per_step": int(step_bytes)},
-    }), flush=True)
+    }
+    if not args.no_cpu_baseline:
+        log("CPU baseline: one window-1024 call and one global call of the stack on host cores")
+        result["cpu_baseline"] = cpu_mixed_baseline(cache, qs[0, 0], ks[0, 0], vs[0, 0], windows)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_mixed_baseline(cache, q, k, v, windows, budget_s=15.0):
+    """The restated reference fallback (append + masked SDPA with GQA, torch CPU) for one call of
+    each kind the stack makes -- window 1024 and global, B=16 rows at position 4096 -- and a step
+    priced as the stack's mix of them (18 windowed calls, 6 global)."""
+    import torch
+    from oracle import sdpa_fallback
+
+    cores = host_cores()
+    torch.set_num_threads(cores)
+    kc, vc = cache.k_cache[0, :, :MX_P + 1].cpu(), cache.v_cache[0, :, :MX_P + 1].cpu()
+    qc, kn, vn = q.cpu(), k.cpu(), v.cpu()
+    pos = torch.full((MX_B,), MX_P, dtype=torch.int32)
+    per = {}
+    t_end = time.perf_counter() + budget_s
+    for w in (MX_WIN, -1):
+        times = []
+        sdpa_fallback.flash_attn_with_kvcache(qc, kc, vc, kn, vn, pos, (w, 0))  # warm-up
+        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+            t0 = time.perf_counter()
+            sdpa_fallback.flash_attn_with_kvcache(qc, kc, vc, kn, vn, pos, (w, 0))
+            times.append(time.perf_counter() - t0)
+        per[w] = (statistics.median(times), len(times))
+    step = sum(per[w][0] for w in windows)
+    return {"value": round(MX_B / step, 1), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"one window-{MX_WIN} call (median of {per[MX_WIN][1]}) and one global call "
+                      f"(median of {per[-1][1]}) at B={MX_B}, position {MX_P}; step = "
+                      f"{sum(w >= 0 for w in windows)} windowed + {sum(w < 0 for w in windows)} "
+                      f"global calls; torch CPU SDPA restatement of the reference fallback"}
 
 
 SM_LAYERS, SM_D, SM_H, SM_HKV, SM_HID, SM_V = 32, 4096, 32, 8, 14336, 32768
 SM_PROMPT, SM_ROWS, SM_NEW = 2048, 64, 512
+
+
+def sample_config(n_layers):
+    """The large-batch sampling model: n_layers llama-style blocks, d_model 4096, 32 q / 8 kv
+    heads of 128, gated SiLU MLP 14336, vocab 32768, lm_head softcap 15."""
+    from modelcore_amd.model import ComponentSpec, ModelConfig
+    blocks = [ComponentSpec("block", {
+        "layer_idx": i, "features": [],
+        "mixer": ComponentSpec("attention", {"n_head": SM_H, "n_kv_head": SM_HKV, "head_dim": D,
+                                             "window": -1, "kv_slot": None, "produces_kv": True,
+                                             "features": []}),
+        "ffn": ComponentSpec("gated_mlp", {"activation": "silu", "hidden_dim": SM_HID})})
+        for i in range(n_layers)]
+    return ModelConfig(sequence_len=SM_PROMPT + SM_NEW, vocab_size=SM_V, n_embd=SM_D,
+                       shared={"rope": ComponentSpec("rotary", {"head_dim": D, "over_compute": 2}),
+                               "norm": ComponentSpec("rms_norm", {"eps": None})},
+                       input=ComponentSpec("token_embedding", {"smear": False}),
+                       body=ComponentSpec("stack", {"blocks": blocks, "features": []}),
+                       output=ComponentSpec("lm_head", {"softcap": 15}))
+
+
+def cpu_sample_baseline(budget_s=20.0):
+    """The reference's decode step on the host, restated: the same model on the CPU in fp32 (the
+    reference's CPU compute dtype, modelcore/runtime.py:23-42) with the restated SDPA fallback as
+    its operator, 64 rows at position 2048 of a 2560-position cache. One layer is built (seed 0)
+    and its step timed with and without the layer's work, and the 32-layer step priced as
+    32 layers + embedding and lm_head."""
+    import torch
+    from modelcore_amd.model import ModelManager
+    from modelcore_amd.runtime import Runtime
+    from oracle import sdpa_fallback
+
+    cores = host_cores()
+    torch.set_num_threads(cores)
+    mgr = ModelManager(Runtime(torch.float32), attention=sdpa_fallback.flash_attn)
+    model = mgr.create_model(sample_config(1), device=torch.device("cpu"), seed=0)
+    cache = mgr.new_kv_cache(model, batch_size=SM_ROWS, seq_len=SM_PROMPT + SM_NEW)
+    g = torch.Generator().manual_seed(0)
+    cache.k_cache[:, :, :SM_PROMPT].copy_(torch.randn(cache.k_cache[:, :, :SM_PROMPT].shape,
+                                                      generator=g))
+    cache.v_cache[:, :, :SM_PROMPT].copy_(torch.randn(cache.v_cache[:, :, :SM_PROMPT].shape,
+                                                      generator=g))
+    tokens = torch.randint(0, SM_V, (SM_ROWS, 1), generator=g)
+
+    def timed(fn, n_min=3, n_max=20, until=None):
+        times = []
+        fn()  # warm-up
+        while len(times) < n_min or (time.perf_counter() < until and len(times) < n_max):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times), len(times)
+
+    def step():
+        cache.cache_seqlens.fill_(SM_PROMPT)
+        cache._pos_uniform = SM_PROMPT
+        model(tokens, kv_cache=cache)
+
+    x = model.embedding(tokens)
+    t_end = time.perf_counter() + budget_s
+    with torch.no_grad():
+        t_step, n_step = timed(step, until=t_end - budget_s / 3)
+        t_head, n_head = timed(lambda: model.unembedding(x), until=t_end)
+    t_layer = max(t_step - t_head, 0.0)
+    step_32 = SM_LAYERS * t_layer + t_head
+    return {"value": round(SM_ROWS / step_32, 2), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"one decode step of a 1-layer copy of the model (fp32, oracle operator: the "
+                      f"restated reference fallback), 64 rows at position {SM_PROMPT}, median of "
+                      f"{n_step}; lm_head alone median of {n_head}; step = {SM_LAYERS} x "
+                      f"({t_layer * 1e3:.1f} ms per layer) + {t_head * 1e3:.1f} ms head"}
 
 
 def bench_sample(args):
@@ -384,26 +615,14 @@ def bench_sample(args):
     untimed; the value is rows x timed steps / time."""
     import torch
     from modelcore_amd import stats
-    from modelcore_amd.model import ComponentSpec, ModelConfig, ModelManager
+    from modelcore_amd.model import ModelManager
     from modelcore_amd.runtime import Runtime
     from modelcore_amd.sampling import PhiloxSampler
 
     dev = torch.device("cuda", 0)
     W = min(args.warmup, SM_NEW - 1)
     K = SM_NEW - W
-    blocks = [ComponentSpec("block", {
-        "layer_idx": i, "features": [],
-        "mixer": ComponentSpec("attention", {"n_head": SM_H, "n_kv_head": SM_HKV, "head_dim": D,
-                                             "window": -1, "kv_slot": None, "produces_kv": True,
-                                             "features": []}),
-        "ffn": ComponentSpec("gated_mlp", {"activation": "silu", "hidden_dim": SM_HID})})
-        for i in range(SM_LAYERS)]
-    cfg = ModelConfig(sequence_len=SM_PROMPT + SM_NEW, vocab_size=SM_V, n_embd=SM_D,
-                      shared={"rope": ComponentSpec("rotary", {"head_dim": D, "over_compute": 2}),
-                              "norm": ComponentSpec("rms_norm", {"eps": None})},
-                      input=ComponentSpec("token_embedding", {"smear": False}),
-                      body=ComponentSpec("stack", {"blocks": blocks, "features": []}),
-                      output=ComponentSpec("lm_head", {"softcap": 15}))
+    cfg = sample_config(SM_LAYERS)
     mgr = ModelManager(Runtime(torch.bfloat16))
     log(f"building the {SM_LAYERS}-layer model on the GPU (seed 0)")
     model = mgr.create_model(cfg, device=dev, seed=0)
@@ -451,7 +670,8 @@ def bench_sample(args):
              for i in range(K)) / K * SM_LAYERS
     step_bytes = weight_bytes + kv
     gbps = step_bytes / (ms * 1e-3) / 1e9
-    print(json.dumps({
+    hbm_peak, _, peak_src = peaks()
+    result = {
         "metric": "large-batch sampling tok/s: 32-layer 4096-wide model, one 2048-token prompt "
                   "replicated to 64 rows, 512 tokens per row at temperature 1",
         "value": round(SM_ROWS / (ms * 1e-3), 1), "unit": "tok/s", "n_gpus": 1, "steps": K,
@@ -469,10 +689,14 @@ def bench_sample(args):
                    "prefill_and_replicate_ms": round(prefill_ms, 2)},
         "roofline": {"kernel": "whole decode step (bf16 weight GEMMs + cached attention of 32 "
                                "layers + sampling)", "bound": "hbm", "achieved": round(gbps, 1),
-                     "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(gbps * 1e9 / HBM_PEAK, 4), "traffic": None,
+                     "peak": hbm_peak / 1e9, "peak_source": peak_src, "unit": "GB/s",
+                     "frac": round(gbps * 1e9 / hbm_peak, 4), "traffic": None,
                      "bytes_per_step": int(step_bytes), "weight_bytes": int(weight_bytes)},
-    }), flush=True)
+    }
+    if not args.no_cpu_baseline:
+        log("CPU baseline: one decode step of a 1-layer copy of the model on host cores")
+        result["cpu_baseline"] = cpu_sample_baseline()
+    print(json.dumps(result), flush=True)
 
 
 def cpu_baseline(kc, vc, q, k, v, seqlens, budget_s=12.0):
@@ -481,7 +705,7 @@ def cpu_baseline(kc, vc, q, k, v, seqlens, budget_s=12.0):
     import torch
     from oracle import sdpa_fallback
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = host_cores()
     torch.set_num_threads(cores)
     kc, vc = kc.clone(), vc.clone()
     times = []
@@ -501,6 +725,12 @@ def main():
               f"with no cross-GPU exchange, so run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    if args.summarize_traffic:
+        summarize_traffic(*args.summarize_traffic)
+        return
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace, args.launches)
+        return
     if args.calibrate_copy:
         calibrate_copy()
         return
@@ -528,6 +758,7 @@ def main():
     log(f"generating inputs: B={B} H={H} H_kv={H_KV} D={D} T_alloc={t_alloc} steps={W}+{K}")
     g = torch.Generator().manual_seed(args.seed)
     seqlens = torch.randint(L_MIN, L_MAX + 1, (B,), generator=g, dtype=torch.int32)
+    assert torch.equal(seqlens, drawn_lengths(args.seed))
     kc = torch.randn(B, t_alloc, H_KV, D, generator=g).to(torch.bfloat16)
     vc = torch.randn(B, t_alloc, H_KV, D, generator=g).to(torch.bfloat16)
     qs = torch.randn(W + K, B, 1, H, D, generator=g).to(torch.bfloat16)
@@ -585,15 +816,16 @@ def main():
     # Dominant kernels: the decode call of one step as the step issues it -- append of the new
     # token fused into the split-K streaming pass (decode_fused_kernel), then the merge pass
     # (decode_merge_kernel) -- launched back to back through the C ABI on the stream they run on
-    # and timed with HIP events around N launches. The positions stay put, so every launch
-    # rewrites the same new token and reads the same keys. Launches alternate between this cache
-    # and a second one of the same shape (as consecutive layers of a model would), so no launch
-    # finds the previous launch's keys in the 256 MB memory-side cache.
+    # and timed with HIP events around ROOF_LAUNCHES launches. Every launch puts each row's query
+    # at its drawn length (whatever --steps and --warmup are) and appends there, so every launch
+    # reads the same keys. Launches alternate between this cache and a second one of the same
+    # shape (as consecutive layers of a model would), so no launch finds the previous launch's
+    # keys in the 256 MB memory-side cache.
     lib = _ext.lib()
-    pos = cache.cache_seqlens  # positions now: base + W + K, each row's query at its position
+    pos = seqlens.to(dev)
     out = torch.empty(B, 1, H, D, dtype=torch.bfloat16, device=dev)
     ws_bytes = lib.mcamd_attn_workspace_bytes(B, 1, H, H_KV, D, t_alloc, -1)
-    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     stream = _ext.stream_handle(dev)
     q1, k1, v1 = qd[0], kd[0], vd[0]
     other = torch.randn(2, *k_slot.shape, device=dev,
@@ -609,18 +841,18 @@ def main():
 
     for i in range(6):
         _ext.check(decode_call(i), "flash_attn_with_kvcache")
-    n_attn = max(K, 50)
     torch.cuda.synchronize()
     start.record()
-    for i in range(n_attn):
+    for i in range(ROOF_LAUNCHES):
         decode_call(i)
     end.record()
     torch.cuda.synchronize()
-    attn_us = start.elapsed_time(end) / n_attn * 1e3
-    attn_positions = final.tolist()
-    attn_bytes = stats.decode_step_bytes(attn_positions, H, H_KV, D, 2, append=True)
+    attn_us = start.elapsed_time(end) / ROOF_LAUNCHES * 1e3
+    attn_bytes = stats.decode_step_bytes(base, H, H_KV, D, 2, append=True)
+    assert attn_bytes == roofline_bytes(args.seed)
     attn_gbps = attn_bytes / (attn_us * 1e-6) / 1e9
-    traffic = measured_traffic()
+    traffic, traffic_src = measured_traffic(attn_bytes) if args.seed == 0 else (None, "seed != 0")
+    hbm_peak, _, peak_src = peaks()
 
     result = {
         "metric": METRIC,
@@ -643,17 +875,21 @@ def main():
             "timing": "eager" if args.eager else "hip_graph",
         },
         "kv_path_gbps": round(step_gbps, 1),
-        "kv_path_pct_peak": round(100 * step_gbps * 1e9 / HBM_PEAK, 2),
+        "kv_path_pct_peak": round(100 * step_gbps * 1e9 / hbm_peak, 2),
         "roofline": {
             "kernel": "decode_fused_kernel + decode_merge_kernel (append + attention)",
             "bound": "hbm",
             "achieved": round(attn_gbps, 1),
-            "peak": HBM_PEAK / 1e9,
+            "peak": hbm_peak / 1e9,
+            "peak_source": peak_src,
             "unit": "GB/s",
-            "frac": round(attn_gbps * 1e9 / HBM_PEAK, 4),
+            "frac": round(attn_gbps * 1e9 / hbm_peak, 4),
             "traffic": traffic,
+            "traffic_source": traffic_src,
             "us_per_launch": round(attn_us, 2),
             "bytes_per_launch": attn_bytes,
+            "launches": ROOF_LAUNCHES,
+            "positions": "the drawn lengths (seed 0), the same for every launch",
         },
     }
 

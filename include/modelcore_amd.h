@@ -112,7 +112,7 @@ int mcamd_flash_attn_with_kvcache(const void *q, const void *k, const void *v,
  * stream's device must be the current device. Otherwise identical to
  * mcamd_flash_attn_with_kvcache, with the same kernels and bit-identical results.
  */
-#define MCAMD_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+#define MCAMD_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int mcamd_flash_attn_with_kvcache_noalloc(const void *q, const void *k, const void *v,
                                           void *k_cache, void *v_cache,
                                           const int32_t *cache_seqlens, void *out, int64_t batch,
@@ -145,18 +145,19 @@ int mcamd_prefill_attention(const void *q, const void *k_cache, const void *v_ca
 
 /*
  * Next-token sampling on the device, one token per row of `logits` ((batch, vocab) fp32, rows
- * `row_stride` elements apart; 0 = every row reads the same logits): temperature 0 takes the argmax (lowest index on ties); otherwise
- * the Gumbel-max draw from softmax(logits / temperature) with Philox4x32-10 noise keyed by the
- * row's 64-bit `seeds[b]` at counter offsets[b], which the call then advances by one (device
- * side, no host sync). Writes int64 token ids to out[b].
- * Replaces sample_next_token's softmax + torch.multinomial (modelcore/generate.py:18-34); the
- * per-row counter stream stands in for its single torch.Generator, so a row's draws do not depend
- * on the batch it is decoded in. top_k is not supported here (the reference's top_k path stays a
- * torch op in modelcore_amd.generate.sample_next_token).
+ * `row_stride` elements apart; 0 = every row reads the same logits): temperature 0 takes the
+ * argmax (lowest index on ties); otherwise the Gumbel-max draw from softmax(logits / temperature)
+ * with Philox4x32-10 noise keyed by the row's 64-bit `seeds[b]` at counter offsets[b], which the
+ * call then advances by one (device side, no host sync). 0 < top_k < vocab restricts the draw to
+ * the top_k largest logits of the row (ties at the k-th value kept lowest index first); top_k <= 0
+ * or >= vocab draws from all of them. Writes int64 token ids to out[b].
+ * Replaces sample_next_token's softmax + torch.multinomial, and its top_k branch (torch.topk, then
+ * the draw over the kept logits) (modelcore/generate.py:18-34); the per-row counter stream stands
+ * in for its single torch.Generator, so a row's draws do not depend on the batch it is decoded in.
  */
 int mcamd_sample_tokens(const float *logits, int64_t batch, int64_t vocab, int64_t row_stride,
-                        float temperature, const uint64_t *seeds, int64_t *offsets, int64_t *out,
-                        void *stream);
+                        float temperature, int64_t top_k, const uint64_t *seeds, int64_t *offsets,
+                        int64_t *out, void *stream);
 
 /*
  * The step before the operator, fused: RoPE at each token's position p = cache_seqlens[b] + t,

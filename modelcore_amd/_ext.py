@@ -23,7 +23,7 @@ F32, BF16 = 0, 1
 ACT_SILU = 0  # mcamd_linear_bf16_gated activations
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH = 0, -1, -2, -3, -4
 ABI_VERSION = 5
-NOALLOC_SCRATCH_BYTES = 16 << 20  # MCAMD_NOALLOC_SCRATCH_BYTES
+NOALLOC_SCRATCH_BYTES = 32 << 20  # MCAMD_NOALLOC_SCRATCH_BYTES
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -49,8 +49,8 @@ SIGNATURES = {
                                       _i64, _i64, _int, _ptr, _size, _ptr]),
     "mcamd_prefill_attention": (_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64,
                                        _i64, _i64, _i64, _i64, _int, _ptr]),
-    "mcamd_sample_tokens": (_int, [_ptr, _i64, _i64, _i64, ctypes.c_float, _ptr, _ptr, _ptr,
-                                   _ptr]),
+    "mcamd_sample_tokens": (_int, [_ptr, _i64, _i64, _i64, ctypes.c_float, _i64, _ptr, _ptr,
+                                   _ptr, _ptr]),
     "mcamd_qk_rope_norm_append": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _i64,
                                          _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64,
                                          _i64, _i64, ctypes.c_float, ctypes.c_float, _int,

@@ -157,6 +157,14 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// The power of two (16 to 256) whose kernel instantiation serves head_dim d, or 0 past 256.
+inline int head_dim_bucket(int64_t d) {
+  if (d > 256) return 0;
+  int p = 16;
+  while (p < d) p *= 2;
+  return p;
+}
+
 // Key range of the query at position p under a left window (w < 0 = unlimited): [lo, p].
 __device__ __forceinline__ int key_lo(int p, int window) {
   return window >= 0 ? max(0, p - window) : 0;

@@ -39,17 +39,20 @@ struct DecodeParams {
   float scale_log2;
 };
 
-template <class E, int D, int GM>
+// DP is head_dim rounded up to a power of two (at least 16): LPT = DP / VEC lanes cover one key
+// row, and lanes past the real head_dim D hold nothing (they load no data and add zeros).
+template <class E, int DP, int GM>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams P) {
   constexpr int VEC = Vec<E>::N;
-  constexpr int LPT = D / VEC;         // lanes per key row
+  constexpr int LPT = DP / VEC;        // lanes per key row
   constexpr int TPI = kThreads / LPT;  // keys per pass of the workgroup
   constexpr int U = 4;                 // keys in flight per thread
   static_assert(LPT >= 1 && LPT <= 64 && (64 % LPT) == 0, "head_dim too large for one wave");
+  const int D = P.D;
 
   __shared__ float s_p[GM][SL];
   __shared__ float s_m[GM], s_l[GM];
-  __shared__ float s_red[kWaves][GM][D];
+  __shared__ float s_red[kWaves][GM][DP];
 
   const int split = blockIdx.x;
   const int kvh = blockIdx.y / P.n_hchunks;
@@ -70,6 +73,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams P) 
   const int tg = tid / LPT;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const bool live = li * VEC < D;  // this lane holds dims of the head
 
   const E *q = static_cast<const E *>(P.q);
   const E *kc = static_cast<const E *>(P.k_cache);
@@ -83,7 +87,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams P) 
   float qv[GM][VEC];
 #pragma unroll
   for (int g = 0; g < GM; ++g) {
-    if (g < gcount) {
+    if (g < gcount && live) {
       float x[VEC];
       Vec<E>::load(q + (int64_t(b) * P.H + h0 + g) * D + li * VEC, x);
 #pragma unroll
@@ -100,7 +104,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams P) 
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int r = r0 + u * TPI;
-      if (r < n) {
+      if (r < n && live) {
         const int t = t0 + r;
         const E *src = (t == pos && kn) ? kn + new_off : kc + row_base + int64_t(t) * tok_stride;
         Vec<E>::unpack(load_stream(src), kx[u]);  // K/V are read once per pass
@@ -159,10 +163,13 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams P) 
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int r = r0 + u * TPI;
-      if (r < n) {
+      if (r < n && live) {
         const int t = t0 + r;
         const E *src = (t == pos && vn) ? vn + new_off : vc + row_base + int64_t(t) * tok_stride;
         Vec<E>::unpack(load_stream(src), vx[u]);  // K/V are read once per pass
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) vx[u][e] = 0.f;
       }
     }
 #pragma unroll
@@ -238,35 +245,37 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeParams P) {
   }
 }
 
-template <class E, int D, int GM>
+template <class E, int DP, int GM>
 int run_decode(const DecodeParams &P, int B, hipStream_t stream) {
   dim3 grid(P.n_splits, P.H_kv * P.n_hchunks, B);
-  hipLaunchKernelGGL((decode_split_kernel<E, D, GM>), grid, dim3(kThreads), 0, stream, P);
+  hipLaunchKernelGGL((decode_split_kernel<E, DP, GM>), grid, dim3(kThreads), 0, stream, P);
   int st = launch_status("decode_split");
   if (st != MCAMD_OK) return st;
   hipLaunchKernelGGL(decode_combine_kernel<E>, dim3(P.H, B), dim3(128), 0, stream, P);
   return launch_status("decode_combine");
 }
 
-template <class E, int D>
+template <class E, int DP>
 int dispatch_gm(DecodeParams &P, int B, hipStream_t s) {
-  if (P.G == 1) { P.n_hchunks = 1; return run_decode<E, D, 1>(P, B, s); }
-  if (P.G == 2) { P.n_hchunks = 1; return run_decode<E, D, 2>(P, B, s); }
-  if (P.G <= 4) { P.n_hchunks = 1; return run_decode<E, D, 4>(P, B, s); }
+  if (P.G == 1) { P.n_hchunks = 1; return run_decode<E, DP, 1>(P, B, s); }
+  if (P.G == 2) { P.n_hchunks = 1; return run_decode<E, DP, 2>(P, B, s); }
+  if (P.G <= 4) { P.n_hchunks = 1; return run_decode<E, DP, 4>(P, B, s); }
   P.n_hchunks = (P.G + 7) / 8;
-  return run_decode<E, D, 8>(P, B, s);
+  return run_decode<E, DP, 8>(P, B, s);
 }
 
+// Any head_dim up to 256 whose rows are whole 16-byte vectors (checked before), run in the
+// instantiation of the next power of two.
 template <class E>
 int dispatch_d(DecodeParams &P, int B, hipStream_t s) {
-  switch (P.D) {
+  switch (head_dim_bucket(P.D)) {
     case 16: return dispatch_gm<E, 16>(P, B, s);
     case 32: return dispatch_gm<E, 32>(P, B, s);
     case 64: return dispatch_gm<E, 64>(P, B, s);
     case 128: return dispatch_gm<E, 128>(P, B, s);
     case 256: return dispatch_gm<E, 256>(P, B, s);
     default:
-      return fail(MCAMD_EUNSUPPORTED, "decode: head_dim must be one of 16, 32, 64, 128, 256");
+      return fail(MCAMD_EUNSUPPORTED, "decode: head_dim must be at most 256");
   }
 }
 

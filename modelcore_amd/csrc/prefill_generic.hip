@@ -1,4 +1,5 @@
-// Multi-token attention against the cache prefix, any head_dim in {16..256}, bf16 or fp32.
+// Multi-token attention against the cache prefix, any head_dim up to 256 made of whole 16-byte
+// vectors, bf16 or fp32.
 //
 // Semantics: modelcore/kernels/flash_attn.py:226-244 (uniform, explicit mask with row offset
 // Tk - Tq) and :362-364 (ragged mask). Query t of row b sits at p = cache_seqlens[b] + t and
@@ -9,8 +10,9 @@
 // MFMA kernel in prefill_mfma.hip takes the large shapes. One workgroup owns 64 (query, head)
 // rows of one KV head: 64 / G consecutive queries times the G query heads that share the KV head,
 // so every K/V tile staged in LDS serves all of them. Four lanes share a row, each owning every
-// fourth dimension. Keys are walked in tiles of 32 from the first key any row of the block can
-// see to the last; each tile's scores are masked per row, and an online softmax (running max m,
+// fourth dimension (of the head_dim rounded up to a power of two; dims past the real head_dim
+// stay zero). Keys are walked in tiles of 32 from the first key any row of the block can see to
+// the last; each tile's scores are masked per row, and an online softmax (running max m,
 // running sum l, rescaled accumulator) folds the tile in.
 #include "kernels.h"
 
@@ -27,17 +29,18 @@ struct PrefillParams {
   const void *q, *k_cache, *v_cache;
   const int32_t *seqlens;
   void *out;
-  int T_new, H, H_kv, G, QT, T_max, window;
+  int T_new, H, H_kv, G, QT, T_max, window, D;
   int64_t cache_b;
   float scale_log2;
 };
 
-template <class E, int D>
+template <class E, int DP>
 __global__ __launch_bounds__(kThreads) void prefill_generic_kernel(PrefillParams P) {
-  constexpr int DS = D / 4;  // dimensions per lane (lane j owns d = 4*i + j)
+  constexpr int DS = DP / 4;  // dimensions per lane (lane j owns d = 4*i + j, d < DP)
   constexpr int VEC = Vec<E>::N;
-  __shared__ float sk[KT][D];
-  __shared__ float sv[KT][D];
+  const int D = P.D;          // the real head_dim (<= DP); dims past it are zero in LDS and q
+  __shared__ float sk[KT][DP];
+  __shared__ float sv[KT][DP];
 
   const int qt0 = blockIdx.x * P.QT;
   const int kvh = blockIdx.y;
@@ -60,15 +63,23 @@ __global__ __launch_bounds__(kThreads) void prefill_generic_kernel(PrefillParams
 
   if (!row_ok) {
     if (active)
-      for (int i = 0; i < DS; ++i) out[out_off + 4 * i + j] = from_f32<E>(NAN);
+      for (int i = 0; i < DS; ++i)
+        if (4 * i + j < D) out[out_off + 4 * i + j] = from_f32<E>(NAN);
     return;
   }
+  // Columns past the head_dim: zero once; the tile staging below writes columns < D only.
+  if (D < DP)
+    for (int c = tid; c < KT * DP; c += kThreads)
+      if (c % DP >= D) {
+        sk[c / DP][c % DP] = 0.f;
+        sv[c / DP][c % DP] = 0.f;
+      }
 
   const int p = pos + tq;  // this row's query position
   float qv[DS], o[DS];
 #pragma unroll
   for (int i = 0; i < DS; ++i) {
-    qv[i] = active ? to_f32<E>(q[out_off + 4 * i + j]) * P.scale_log2 : 0.f;
+    qv[i] = active && 4 * i + j < D ? to_f32<E>(q[out_off + 4 * i + j]) * P.scale_log2 : 0.f;
     o[i] = 0.f;
   }
   float m = -INFINITY, l = 0.f;
@@ -141,27 +152,28 @@ __global__ __launch_bounds__(kThreads) void prefill_generic_kernel(PrefillParams
   if (active) {
     const float inv = 1.f / l;
 #pragma unroll
-    for (int i = 0; i < DS; ++i) out[out_off + 4 * i + j] = from_f32<E>(o[i] * inv);
+    for (int i = 0; i < DS; ++i)
+      if (4 * i + j < D) out[out_off + 4 * i + j] = from_f32<E>(o[i] * inv);
   }
 }
 
-template <class E, int D>
+template <class E, int DP>
 int run_prefill(const PrefillParams &P, int B, hipStream_t stream) {
   dim3 grid((P.T_new + P.QT - 1) / P.QT, P.H_kv, B);
-  hipLaunchKernelGGL((prefill_generic_kernel<E, D>), grid, dim3(kThreads), 0, stream, P);
+  hipLaunchKernelGGL((prefill_generic_kernel<E, DP>), grid, dim3(kThreads), 0, stream, P);
   return launch_status("prefill_generic");
 }
 
 template <class E>
 int dispatch_d(const PrefillParams &P, int D, int B, hipStream_t s) {
-  switch (D) {
+  switch (head_dim_bucket(D)) {
     case 16: return run_prefill<E, 16>(P, B, s);
     case 32: return run_prefill<E, 32>(P, B, s);
     case 64: return run_prefill<E, 64>(P, B, s);
     case 128: return run_prefill<E, 128>(P, B, s);
     case 256: return run_prefill<E, 256>(P, B, s);
     default:
-      return fail(MCAMD_EUNSUPPORTED, "prefill: head_dim must be one of 16, 32, 64, 128, 256");
+      return fail(MCAMD_EUNSUPPORTED, "prefill: head_dim must be at most 256");
   }
 }
 
@@ -183,6 +195,7 @@ int launch_prefill_generic(const AttnArgs &a) {
   P.T_max = int(a.t_max);
   P.window = int(a.window < 0 ? -1 : a.window);
   P.cache_b = a.cache_batch_stride;
+  P.D = int(a.head_dim);
   P.scale_log2 = float(kLog2e / std::sqrt(double(a.head_dim)));
   if (a.dtype == MCAMD_BF16) return dispatch_d<bf16>(P, int(a.head_dim), int(a.batch), a.stream);
   return dispatch_d<float>(P, int(a.head_dim), int(a.batch), a.stream);

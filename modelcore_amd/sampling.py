@@ -10,9 +10,10 @@ that each call advances, so:
 * nothing is read back to the host, so a decode step that samples stays asynchronous.
 
 This is the sampling half of modelcore/generate.py:18-34 (``sample_next_token`` with
-temperature > 0 and no top_k) restated for the device; the reference draws from one
+temperature > 0, with or without top_k) restated for the device; the reference draws from one
 torch.Generator for the whole batch, which has no per-row meaning. Temperature 0 is the argmax,
-as in the reference.
+as in the reference. With top_k the draw is over the k largest logits of each row (ties at the
+k-th value kept lowest index first).
 """
 from __future__ import annotations
 
@@ -33,7 +34,7 @@ class PhiloxSampler:
                                   device=device)
         self.offsets = torch.zeros(batch_size, dtype=torch.int64, device=device)
 
-    def __call__(self, logits, temperature=1.0):
+    def __call__(self, logits, temperature=1.0, top_k=None):
         """(B, V) logits -> (B, 1) int64 token ids; advances every row's counter by one."""
         _ext.require_rocm(logits, what="PhiloxSampler")
         if logits.dim() != 2 or logits.size(0) != self.batch_size:
@@ -47,7 +48,8 @@ class PhiloxSampler:
         out = torch.empty(self.batch_size, dtype=torch.int64, device=logits.device)
         st = _ext.lib().mcamd_sample_tokens(
             logits.data_ptr(), self.batch_size, logits.size(1), logits.stride(0),
-            float(temperature), self.seeds.data_ptr(), self.offsets.data_ptr(), out.data_ptr(),
+            float(temperature), int(top_k or 0), self.seeds.data_ptr(), self.offsets.data_ptr(),
+            out.data_ptr(),
             _ext.stream_handle(logits.device))
         _ext.check(st, "sample_tokens")
         return out.view(-1, 1)

@@ -8,6 +8,9 @@ word i % 4 of Philox(counter = (i // 4, o low, o high, 0), key = seed_b low/high
 u = ((x >> 9) + 1/2) / 2^23, score = logit / T - log(-log(u)); the draw is the first index of the
 maximum. It is the reference's softmax(logits / T) sampling (modelcore/generate.py:18-34) in
 Gumbel-max form, with a per-row counter-based stream in place of torch.multinomial's generator.
+With top_k, only the k largest logits take part (`top_k_mask`: ties at the k-th value kept lowest
+index first), the reference's top_k branch (generate.py:23-29: torch.topk, then the draw over the
+kept values).
 """
 from __future__ import annotations
 
@@ -48,23 +51,40 @@ def uniforms(seed, offset, vocab):
     return ((words >> np.uint64(9)).astype(np.float64) + 0.5) / 8388608.0
 
 
-def scores(logits, seed, offset, temperature):
-    """Gumbel-perturbed scores of one row, float64."""
+def top_k_mask(logits, top_k):
+    """(V,) bool: the top_k largest logits of the row, ordered by value then by lowest index (NaN
+    after -inf, -0 equal to +0); all of them when top_k is None, <= 0 or >= V."""
+    logits = np.asarray(logits, dtype=np.float64)
+    V = logits.size
+    keep = np.zeros(V, dtype=bool)
+    if top_k is None or top_k <= 0 or top_k >= V:
+        keep[:] = True
+        return keep
+    key = np.where(np.isnan(logits), -np.inf, logits)
+    nan = np.isnan(logits)
+    order = np.lexsort((np.arange(V), nan, -key))  # value descending, NaN last, then index
+    keep[order[:top_k]] = True
+    return keep
+
+
+def scores(logits, seed, offset, temperature, top_k=None):
+    """Gumbel-perturbed scores of one row, float64 (-inf outside the top_k set)."""
     logits = np.asarray(logits, dtype=np.float64)
     if temperature == 0:
         return logits
     u = uniforms(seed, offset, logits.size)
-    return logits / temperature - np.log(-np.log(u))
+    s = logits / temperature - np.log(-np.log(u))
+    return np.where(top_k_mask(logits, top_k), s, -np.inf)
 
 
-def sample(logits, seeds, offsets, temperature):
+def sample(logits, seeds, offsets, temperature, top_k=None):
     """(B,) token ids for (B, V) logits; returns (ids, margins) where a margin is the gap between
     the best and second-best score of the row (a device float32 evaluation can only differ from
     this float64 one when the gap is within rounding)."""
     logits = np.asarray(logits, dtype=np.float64)
     ids, margins = [], []
     for b in range(logits.shape[0]):
-        s = scores(logits[b], int(seeds[b]), int(offsets[b]), temperature)
+        s = scores(logits[b], int(seeds[b]), int(offsets[b]), temperature, top_k)
         order = np.argsort(-s, kind="stable")
         ids.append(int(order[0]))
         margins.append(float(s[order[0]] - s[order[1]]) if s.size > 1 else np.inf)

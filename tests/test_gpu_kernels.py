@@ -165,6 +165,11 @@ DECODE_CASES = [
     ([1999, 0, 1], 16, 4, 128, 2000, 5),    # tiny windows in a long cache
     (RAGGED_80, 16, 4, 128, 700, -1),       # more rows than one wave scans
     (RAGGED_80, 16, 4, 128, 700, 100),
+    # head dims that are not powers of two: run by the next power's kernel, lanes past D idle
+    ([37, 300, 0, 511], 16, 4, 80, 520, -1),
+    ([100, 7], 12, 4, 96, 128, 33),
+    ([300, 5, 77], 8, 2, 192, 320, -1),
+    ([60, 3], 4, 4, 48, 64, -1),
 ]
 
 
@@ -259,6 +264,9 @@ PREFILL_CASES = [
     ([5, 400], 40, 16, 2, 128, 448, 64),          # G = 8
     ([1000], 64, 16, 1, 128, 1100, -1),           # G = 16: 16 positions per workgroup
     ([7, 0], 1, 32, 8, 128, 16, -1),              # a single query through the prefill path
+    ([17, 3], 25, 16, 4, 80, 64, -1),             # head dims that are not powers of two
+    ([100, 0, 31], 70, 12, 4, 96, 200, 50),
+    ([5, 40], 33, 8, 2, 192, 80, -1),
 ]
 
 

@@ -61,3 +61,54 @@ def test_the_device_sampler_refuses_cpu_tensors():
     from modelcore_amd.sampling import PhiloxSampler
     with pytest.raises(RuntimeError, match="ROCm device"):
         PhiloxSampler(2, torch.device("cpu"))
+
+
+def test_top_k_mask_against_a_sort_with_ties():
+    """The kept set is the k largest values, ties at the k-th value kept lowest index first --
+    checked against a plain sort of (value, index) pairs on rows full of ties, and NaN kept last."""
+    g = np.random.default_rng(1)
+    for _ in range(200):
+        V = int(g.integers(2, 40))
+        row = g.integers(-3, 4, V).astype(np.float64)  # many equal values
+        if g.random() < 0.2:
+            row[g.integers(0, V)] = np.nan
+        k = int(g.integers(1, V + 2))
+        nan = np.isnan(row)
+        pairs = sorted(range(V), key=lambda i: (np.inf if nan[i] else -row[i], bool(nan[i]), i))
+        want = np.zeros(V, dtype=bool)
+        want[pairs[:min(k, V)]] = True
+        assert np.array_equal(S.top_k_mask(row, k), want), (row, k)
+    assert S.top_k_mask(np.array([5.0, 3, 3, 3, 1]), 2).tolist() == [True, True, False, False, False]
+    assert S.top_k_mask(np.array([np.nan, -np.inf, 0.0]), 2).tolist() == [False, True, True]
+    assert S.top_k_mask(np.array([1.0, -0.0, 0.0]), 2).tolist() == [True, True, False]
+    assert S.top_k_mask(np.array([1.0, 2.0]), None).all() and S.top_k_mask(np.array([1.0]), 0).all()
+
+
+def test_top_k_draws_follow_softmax_over_the_kept_logits():
+    """The reference's top_k branch (modelcore/generate.py:23-29) draws from softmax(top-k
+    values / T): the restricted Gumbel-max must follow it, and never pick a dropped logit."""
+    logits = np.array([[0.3, -1.0, 2.0, 0.0, 1.1, -0.4, 0.9, -2.0]])
+    k = 3
+    kept = np.argsort(-logits[0])[:k]
+    p = np.zeros(8)
+    p[kept] = np.exp(logits[0, kept] / 0.8)
+    p /= p.sum()
+    n = 20000
+    counts = np.zeros(8)
+    for off in range(n):
+        ids, _ = S.sample(logits, [5], [off], 0.8, top_k=k)
+        counts[ids[0]] += 1
+    assert counts[np.setdiff1d(np.arange(8), kept)].sum() == 0
+    assert np.max(np.abs(counts / n - p)) < 0.015, (counts / n, p)
+
+
+def test_top_k_extremes_reduce_to_plain_draws():
+    g = np.random.default_rng(2)
+    logits = g.standard_normal((5, 64)) * 2
+    seeds, offs = [1, 2, 3, 4, 5], [0, 1, 2, 3, 4]
+    plain, _ = S.sample(logits, seeds, offs, 1.0)
+    for k in (64, 100, 0, None):
+        ids, _ = S.sample(logits, seeds, offs, 1.0, top_k=k)
+        assert np.array_equal(ids, plain)
+    ids, _ = S.sample(logits, seeds, offs, 1.0, top_k=1)
+    assert np.array_equal(ids, np.argmax(logits, axis=1))

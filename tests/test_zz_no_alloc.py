@@ -39,6 +39,8 @@ def _run(entry, c, window, dtype):
 
 CALLS = [
     # seqlens, T_new, H, H_kv, D, T_max, window, dtype: a large call, then smaller ones
+    ([int(x) for x in np.random.default_rng(8).integers(2048, 2560, 64)], 1, 32, 8, 128, 2560, -1,
+     torch.bfloat16),
     ([int(x) for x in np.random.default_rng(9).integers(300, 4000, 32)], 1, 16, 4, 128, 4096, -1,
      torch.bfloat16),
     ([100, 7, 900], 1, 16, 4, 128, 1024, 64, torch.bfloat16),
