@@ -36,6 +36,7 @@ L_MIN, L_MAX = 512, 8192
 COPY_BYTES = 1 << 30
 TRAFFIC_FILE = "profiles/decode_b32_gqa16x4_hd128_ctx8k_traffic.md"
 ROOF_LAUNCHES = 200  # decode calls in the roofline loop
+ROOF_WARMUP_S = 0.1  # seconds of untimed calls before them
 DECODE_KERNELS = ("decode_fused_kernel", "decode_merge_kernel")
 
 
@@ -839,8 +840,19 @@ def main():
             pos.data_ptr(), out.data_ptr(), B, 1, H, H_KV, D, t_alloc, kc_i.stride(0), -1, 1,
             _ext.BF16, ws.data_ptr(), ws_bytes, stream)
 
+    # Warm-up: the first launches over the freshly allocated second cache run ~2 us slower per
+    # call (measured on MI355X: 52.6 us in the first block of 200, 50.6 us after), and a run that
+    # reaches this loop after only a few steps another ~1 us: the timed launches follow
+    # ROOF_WARMUP_S seconds of the same launches, so they are the steady state.
     for i in range(6):
         _ext.check(decode_call(i), "flash_attn_with_kvcache")
+    t_warm = time.perf_counter() + ROOF_WARMUP_S
+    i = 0
+    while time.perf_counter() < t_warm:
+        for _ in range(20):
+            decode_call(i)
+            i += 1
+        torch.cuda.synchronize()
     torch.cuda.synchronize()
     start.record()
     for i in range(ROOF_LAUNCHES):

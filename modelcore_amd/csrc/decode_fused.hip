@@ -57,7 +57,7 @@ constexpr int kMaxGroups = 1024;      // 4-wave workgroups per launch, at most
 #endif
 constexpr int kGroupsPerCU = MCAMD_DECODE_GROUPS_PER_CU;  // 1: one wave per SIMD
 #ifndef MCAMD_DECODE_MIN_KEYS
-#define MCAMD_DECODE_MIN_KEYS 64
+#define MCAMD_DECODE_MIN_KEYS 72
 #endif
 constexpr int kMinKeysPerGroup = MCAMD_DECODE_MIN_KEYS;  // fewer workgroups when the job is small
 #ifndef MCAMD_DECODE_RING
@@ -72,7 +72,7 @@ static_assert(NW == 4 || NW == 8, "the four-row merge at a segment end takes 4 o
 constexpr int kMergeSplit = NW / 4;          // waves per KV-head row in that merge
 constexpr int kMergeDims = 128 / 16 / kMergeSplit;  // dims per lane in that merge (8 or 4)
 #ifndef MCAMD_DECODE_SEG_COST
-#define MCAMD_DECODE_SEG_COST 96
+#define MCAMD_DECODE_SEG_COST 64
 #endif
 constexpr int kSegCost = MCAMD_DECODE_SEG_COST;  // key-free lead slots per unit (see unit_span)
 constexpr int kPart = KG * GM * D + 2 * KG * GM;  // floats per partial: o[16][D], (m, l)[16]
