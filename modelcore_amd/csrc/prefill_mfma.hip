@@ -354,6 +354,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
       }
     } else {
       const int t = ph / 2 - 1;  // M(t)
+      // The matrix phase at raised wave priority: when the matrix core frees, the SIMD issues
+      // this wave's next product before its partner's VALU work (measured: +1.4-2.3% on the 16K
+      // chunked prefill; the opposite preference costs 7%).
+      __builtin_amdgcn_s_setprio(1);
       if (t + 1 < n_tiles) {
         // The two products interleaved; the twelve LDS reads of step ks + 1 (four K fragments,
         // four V^T fragments of two transpose reads) are issued before the eight products of
@@ -412,6 +416,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
           dma_part(ks);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
     }
   }
 
