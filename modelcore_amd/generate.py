@@ -85,10 +85,11 @@ class Decoder:
         self._logits = self.model.forward(ids, kv_cache=self.kv_cache)[:, -1, :]
         return self._logits
 
-    def capture(self, sampler, temperature=1.0):
+    def capture(self, sampler, temperature=1.0, top_k=None):
         """A ``CapturedStep`` of this decoder: each call samples from the current logits on the
-        device and steps every row, as one graph replay."""
-        return CapturedStep(self, sampler, temperature)
+        device (over the top_k largest logits of each row when top_k is set, as
+        ``sample_next_token``) and steps every row, as one graph replay."""
+        return CapturedStep(self, sampler, temperature, top_k)
 
 
 class CapturedStep:
@@ -111,8 +112,9 @@ class CapturedStep:
     """
 
     @torch.inference_mode()
-    def __init__(self, decoder, sampler, temperature=1.0):
+    def __init__(self, decoder, sampler, temperature=1.0, top_k=None):
         self.decoder, self.sampler, self.temperature = decoder, sampler, float(temperature)
+        self.top_k = top_k
         cache = decoder.kv_cache
         if cache.uniform_pos() is None:
             raise ValueError("CapturedStep needs a uniform cache (rows at one position)")
@@ -125,7 +127,7 @@ class CapturedStep:
                              f"step (RoPE at positions read on the device); layers {unfused} run "
                              f"the separate ops, whose RoPE would stay at the capture's position")
         self._rotary_len = min(b.mixer.rope.cos.size(1) for b in model.body.blocks)
-        self.tokens = sampler(decoder.logits, self.temperature).view(-1, 1).clone()
+        self.tokens = sampler(decoder.logits, self.temperature, self.top_k).view(-1, 1).clone()
         side = torch.cuda.Stream(device=self.tokens.device)
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -151,7 +153,7 @@ class CapturedStep:
     def _body(self):
         logits = self.decoder.model.forward(self.tokens, kv_cache=self.decoder.kv_cache)[:, -1, :]
         self.decoder._logits = logits
-        self.tokens.copy_(self.sampler(logits, self.temperature).view(-1, 1))
+        self.tokens.copy_(self.sampler(logits, self.temperature, self.top_k).view(-1, 1))
 
     def __call__(self):
         """Feed the current token column, sample the next into ``self.tokens`` (returned; it is

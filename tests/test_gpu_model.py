@@ -310,13 +310,15 @@ def test_fused_residual_steps_match_the_separate_ops():
     assert err <= 0.1
 
 
-@pytest.mark.parametrize("fast", [False, True], ids=["library-gemm", "skinny-fused-residual"])
-def test_captured_decode_step_replays_the_eager_steps(fast):
+@pytest.mark.parametrize("fast,top_k", [(False, None), (True, None), (True, 50)],
+                         ids=["library-gemm", "skinny-fused-residual", "skinny-top_k"])
+def test_captured_decode_step_replays_the_eager_steps(fast, top_k):
     """A whole decode step (forward, device sampling, advance) captured once as a HIP graph and
     replayed: the same tokens, logits and cache as the same steps run eagerly, and the host-side
-    position kept in step with the device; also with the skinny GEMM and fused residual steps."""
+    position kept in step with the device; also with the skinny GEMM and fused residual steps,
+    and with the draw restricted to the top_k logits."""
     from modelcore_amd.sampling import PhiloxSampler
-    _note("captured decode step", fast)
+    _note("captured decode step", fast, top_k)
     cfg = mixed_window_config(n_layer=4)
     mgr = gpu_manager(torch.bfloat16)
     model = awake(mgr.create_model(cfg, device=DEV, seed=0))
@@ -330,13 +332,13 @@ def test_captured_decode_step_replays_the_eager_steps(fast):
     sampler = PhiloxSampler(R, DEV, base_seed=7)
     toks, logits = [], []
     for _ in range(n + 1):
-        t = sampler(eager.logits, 1.0).view(-1)
+        t = sampler(eager.logits, 1.0, top_k).view(-1)
         toks.append(t.clone())
         eager.step(t)
         logits.append(eager.logits.float().clone())
 
     dec = mgr.new_decoder(model, prompt.tolist(), num_samples=R, max_tokens=n + 2)
-    step = dec.capture(PhiloxSampler(R, DEV, base_seed=7), 1.0)
+    step = dec.capture(PhiloxSampler(R, DEV, base_seed=7), 1.0, top_k)
     assert torch.equal(step.tokens.view(-1), toks[1])  # the warm-up ran the first step
     assert dec.kv_cache.get_pos() == 90 + 1
     for i in range(1, n):
