@@ -76,3 +76,41 @@ def test_noalloc_refuses_sizes_beyond_its_scratch():
                                                    H, H_kv, D, T_max, T_max * H_kv * D, -1, 1,
                                                    _ext.BF16, None)
     assert st == _ext.EWORKSPACE and b"static array" in lib.mcamd_last_error()
+
+
+def test_noalloc_call_captured_in_a_hip_graph_replays_the_eager_result():
+    """The entry point's purpose: a call recorded under graph capture (it allocates nothing, and
+    records no memset) and replayed, with other calls on the same static scratch between the
+    replays, gives the eager result bit for bit every time."""
+    print("case: noalloc under graph capture", flush=True)
+    lib = _ext.lib()
+    seqlens = [int(x) for x in np.random.default_rng(12).integers(300, 3000, 24)]
+    c = make_case(seqlens, 1, 16, 4, 128, 3072, torch.bfloat16, seed=95)
+    g = {k: v.to(DEV) for k, v in c.items()}
+    out = torch.empty(24, 1, 16, 128, dtype=torch.bfloat16, device=DEV)
+
+    def call():
+        return lib.mcamd_flash_attn_with_kvcache_noalloc(
+            g["q"].data_ptr(), g["k"].data_ptr(), g["v"].data_ptr(), g["k_cache"].data_ptr(),
+            g["v_cache"].data_ptr(), g["cache_seqlens"].data_ptr(), out.data_ptr(), 24, 1, 16, 4,
+            128, 3072, g["k_cache"].stride(0), -1, 1, _ext.BF16, _ext.stream_handle(DEV))
+
+    _ext.check(call(), "noalloc eager")
+    torch.cuda.synchronize()
+    eager = out.clone()
+    k_after = g["k_cache"].clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = call()
+    _ext.check(st, "noalloc captured")
+    other = make_case([900, 50, 2000], 1, 32, 8, 128, 2048, torch.bfloat16, seed=96)
+    for i in range(3):
+        out.fill_(float("nan"))
+        _run("noalloc", other, 64, torch.bfloat16)  # another shape on the same scratch
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+    assert torch.equal(g["k_cache"], k_after)  # the replayed append rewrites the same token
+    assert max_abs(to_np(eager), ko.flash_attn_with_kvcache(
+        to_np(c["q"]), to_np(c["k_cache"]), to_np(c["v_cache"]), to_np(c["k"]), to_np(c["v"]),
+        seqlens, -1)[0]) <= ATOL[torch.bfloat16]
