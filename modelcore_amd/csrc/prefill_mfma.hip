@@ -25,9 +25,11 @@
 // hold them (4h..4h+3, then 8+4h..8+4h+3 for lane half h); the V^T fragment reads the same keys,
 // as two LDS transpose reads of four rows each.
 //
-// Online softmax per pair in fp32 (exp2 domain): the running maximum is raised only when a tile's
-// maximum exceeds it by more than 2^8, so most tiles skip the rescale of O. Tiles entirely inside
-// every pair's visible range skip the masking.
+// Online softmax per pair in fp32 (exp2 domain): a tile's weights are made against the running
+// maximum, and the tile's own maximum is taken (and O rescaled) only when a pair's weights of the
+// tile sum past 2^15 or are not finite, or the pair has no maximum yet -- so most tiles skip both
+// the maximum and the rescale, and weights stay below 2^15. Tiles entirely inside every pair's
+// visible range skip the masking.
 //
 // LDS: four buffers of one K and one V tile (64 keys x 256 bytes each), filled straight from
 // HBM by buffer_load_dwordx4 ... lds (no registers involved) two tiles ahead of their first use;
@@ -57,7 +59,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kPairs = 32 * kWaves;  // (position, head) pairs per workgroup
 constexpr int KT = 64;               // keys per tile
 constexpr int TILE = KT * D;         // elements of one K (or V) tile in LDS
-constexpr float kRescaleSlack = 8.f;
+constexpr float kTileSumLimit = 32768.f;  // 2^15: a pair's weights of one tile sum to at most this
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -245,9 +247,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
         s[mk] = mfma(a, qf[kd], s[mk]);
       }
   };
-  // Masks the keys the pair may not see (tiles that straddle the diagonal or the window edge),
-  // then returns the tile's maximum score of the pair in log2 units.
-  auto mask_max = [&](f32x16 (&s)[2], int k0) {
+  // Masks the keys the pair may not see (tiles that straddle the diagonal or the window edge).
+  auto mask = [&](f32x16 (&s)[2], int k0) {
     const bool need_mask = (k0 + KT - 1 > p_first) || (P.window >= 0 && k0 < p_last - P.window);
     if (need_mask) {
 #pragma unroll
@@ -260,6 +261,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
           if (!ok) s[mk][e] = -INFINITY;
         }
     }
+  };
+  // The tile's maximum score of the pair in log2 units.
+  auto tile_max = [&](const f32x16 (&s)[2]) {
     // Four independent chains, then across the two lane halves on the VALU.
     float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
@@ -282,17 +286,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
     }
   };
   // Weights of 16-key step ks as the P^T fragment (and their sum into l).
-  auto weights = [&](const f32x16 (&s)[2], int ks, float m_use) {
+  auto weights = [&](const f32x16 (&s)[2], int ks, float m_use, float &tl) {
     f32x8 pv;
-    float l2[2] = {0.f, 0.f};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float pe =
-          __builtin_amdgcn_exp2f(fmaf(s[ks >> 1][8 * (ks & 1) + e], P.scale_log2, -m_use));
-      pv[e] = pe;
-      l2[e & 1] += pe;
-    }
-    l += l2[0] + l2[1];
+    for (int e = 0; e < 8; ++e)
+      pv[e] = __builtin_amdgcn_exp2f(fmaf(s[ks >> 1][8 * (ks & 1) + e], P.scale_log2, -m_use));
+    tl += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
     return __builtin_convertvector(pv, bf16x8);
   };
 
@@ -335,8 +334,19 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
       scores(sc, sK[0]);
     } else if (ph & 1) {
       const int t = (ph - 1) / 2;  // V(t)
-      const float mx = mask_max(sc, lo + t * KT);
-      if (__builtin_amdgcn_ballot_w64(mx > m + kRescaleSlack) != 0) {
+      mask(sc, lo + t * KT);
+      // Weights against the running maximum; only when a pair's weights of this tile sum past
+      // 2^15 (or are not finite), or the pair has no maximum yet, is the tile's maximum taken,
+      // the accumulators rescaled and the weights made again.
+      float tl = 0.f;
+      const float m_try = m == -INFINITY ? 0.f : m;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        pk[ks] = weights(sc, ks, m_try, tl);
+        dma_part(ks);
+      }
+      if (__builtin_amdgcn_ballot_w64(!(tl <= kTileSumLimit) || m == -INFINITY) != 0) {
+        const float mx = tile_max(sc);
         const float m_new = fmaxf(m, mx);
         const float alpha = m_new == -INFINITY ? 1.f : exp2_or_zero(m - m_new);
         l *= alpha;
@@ -345,13 +355,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
 #pragma unroll
           for (int e = 0; e < 16; ++e) o[md][e] *= alpha;
         m = m_new;
-      }
-      const float m_use = m == -INFINITY ? 0.f : m;
+        tl = 0.f;
+        const float m_use = m == -INFINITY ? 0.f : m;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        pk[ks] = weights(sc, ks, m_use);
-        dma_part(ks);
+        for (int ks = 0; ks < 4; ++ks) pk[ks] = weights(sc, ks, m_use, tl);
       }
+      l += tl;
     } else {
       const int t = ph / 2 - 1;  // M(t)
       // The matrix phase at raised wave priority: when the matrix core frees, the SIMD issues
