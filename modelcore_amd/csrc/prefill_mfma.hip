@@ -341,10 +341,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
       float tl = 0.f;
       const float m_try = m == -INFINITY ? 0.f : m;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        pk[ks] = weights(sc, ks, m_try, tl);
-        dma_part(ks);
-      }
+      for (int ks = 0; ks < 4; ++ks) pk[ks] = weights(sc, ks, m_try, tl);
+      // The DMA parts after the weights (measured: ~1% faster than interleaved with them).
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) dma_part(ks);
       if (__builtin_amdgcn_ballot_w64(!(tl <= kTileSumLimit) || m == -INFINITY) != 0) {
         const float mx = tile_max(sc);
         const float m_new = fmaxf(m, mx);
