@@ -32,11 +32,12 @@
 //    to bf16 pairs of consecutive tokens; the V rows of the same two tokens are interleaved with
 //    v_perm_b32, so each v_dot2_f32_bf16 adds two tokens' contributions to one output dim.
 //  * Output: a segment that covers its whole unit writes the normalised output; otherwise it
-//    writes (o, m, l) for its 16 heads to workspace slot wave + unit (distinct per segment, since
-//    units advance with the waves), and the merge pass -- one wave per (unit, query head), lane
-//    l owning dims 2l and 2l + 1 -- combines a unit's segments by log-sum-exp. The workgroup
-//    holding a unit's first key records the unit's (first workgroup, segment count), so the
-//    merge pass finds the partials without rebuilding the work split.
+//    writes (o, m, l) for its 16 heads to the workspace -- segment j of unit u in bucket slot
+//    u * 16 + j, segments past the sixteenth in an overflow slot (workgroup + unit, distinct per
+//    segment since units advance with the workgroups) -- and the merge pass -- one wave per
+//    (unit, query head), lane l owning dims 2l and 2l + 1 -- combines a unit's segments by
+//    log-sum-exp. The workgroup holding a unit's first key records the unit's (first workgroup,
+//    segment count), so the merge pass finds the partials without rebuilding the work split.
 //  * Append: the segment that ends at p reads the new token from k/v instead of the cache and
 //    its lanes store it into the cache at p (bit-exact copy; the first query-head group only).
 #include "kernels.h"
