@@ -87,7 +87,9 @@ constexpr int kBucket = MCAMD_DECODE_BUCKET;
 #ifndef MCAMD_DECODE_SPEC
 #define MCAMD_DECODE_SPEC 16
 #endif
-constexpr int kSpec = MCAMD_DECODE_SPEC;  // bucket slots the merge loads before the count is known
+// Bucket slots the merge loads before the count is known, at most; a launch loads fewer (4 or 8)
+// when its units average fewer segments (see launch_decode_fused).
+constexpr int kSpec = MCAMD_DECODE_SPEC;
 static_assert(kSpec <= kBucket, "speculative merge loads stay inside the unit's bucket");
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -736,7 +738,18 @@ int launch_decode_fused(const AttnArgs &a) {
   int st = launch_status("decode_fused");
   if (st != MCAMD_OK) return st;
   const dim3 merge_grid(unsigned(a.batch * P.n_units * KG * GM));
-  hipLaunchKernelGGL(decode_merge_kernel<kSpec>, merge_grid, dim3(64), 0, a.stream, P);
+  // Speculative slot loads sized to the segments a unit is expected to have (about one per
+  // workgroup its keys span, plus the ends): the units of a wide batch span few workgroups, and
+  // loading sixteen slots for them would read mostly unused partials (measured on the 64-row,
+  // 32-layer sampling decode: 6.71 -> 6.62 ms per step with 4 slots; 16 kept where units span
+  // many workgroups, as in the 32-row microbench and the mixed-window stack).
+  const int64_t per_unit = groups / std::max<int64_t>(1, units) + 2;
+  if (kSpec >= 16 && per_unit > 8)
+    hipLaunchKernelGGL(decode_merge_kernel<(kSpec < 16 ? kSpec : 16)>, merge_grid, dim3(64), 0, a.stream, P);
+  else if (per_unit > 4)
+    hipLaunchKernelGGL(decode_merge_kernel<(kSpec < 8 ? kSpec : 8)>, merge_grid, dim3(64), 0, a.stream, P);
+  else
+    hipLaunchKernelGGL(decode_merge_kernel<(kSpec < 4 ? kSpec : 4)>, merge_grid, dim3(64), 0, a.stream, P);
   return launch_status("decode_merge");
 }
 
