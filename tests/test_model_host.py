@@ -186,8 +186,8 @@ def test_seed_zero_init_follows_the_reference_scheme():
     bound = 3 ** 0.5 * 48 ** -0.5
     assert blk.mixer.c_q.weight.abs().max() <= bound and blk.mixer.c_q.weight.std() > bound / 3
     assert not blk.mixer.c_proj.weight.any() and not blk.ffn.down_proj.weight.any()
-    assert abs(float(a.embedding.wte.weight.std()) - 0.8) < 0.05
-    assert abs(float(a.unembedding.lm_head.weight.std()) - 0.001) < 2e-4
+    assert abs(float(a.embedding.wte.weight.detach().std()) - 0.8) < 0.05
+    assert abs(float(a.unembedding.lm_head.weight.detach().std()) - 0.001) < 2e-4
 
 
 def test_the_default_operator_refuses_cpu_tensors():
