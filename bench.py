@@ -284,7 +284,37 @@ def bench_prefill(args):
     attn_ms = start.elapsed_time(end) / K
     flops = sum(stats.prefill_flops([c * PF_C] * PF_B, PF_C, PF_H, D) for c in range(n_chunks))
     achieved = flops / (attn_ms * 1e-3)
-    _, flops_peak, peak_src = peaks()
+    bw_peak, flops_peak, peak_src = peaks()
+
+    # The append alone (kv_append_kernel), the same 32 chunk copies through the C ABI: each moves
+    # its K and V rows in (B, C, H_kv, D) to their cache positions, algorithmic bytes = read +
+    # write of 2 * B * C * H_kv * D bf16 values. A copy takes about as long as one launch through
+    # ctypes, so the 32 launches are captured once as a HIP graph and the replays are timed: the
+    # kernels then run back to back instead of waiting on the host.
+    ks = [kc_new for _, kc_new, _ in chunks]
+    vs = [vc_new for _, _, vc_new in chunks]
+
+    def append_pass(strm):
+        for c in range(n_chunks):
+            _ext.check(lib.mcamd_kv_append(ks[c].data_ptr(), vs[c].data_ptr(), kc.data_ptr(),
+                                           vc.data_ptr(), offs[c].data_ptr(), PF_B, PF_C, PF_HKV,
+                                           D, PF_T, kc.stride(0), _ext.BF16, strm), "append")
+
+    append_pass(stream)
+    torch.cuda.synchronize()
+    append_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(append_graph):
+        append_pass(_ext.stream_handle(dev))
+    append_graph.replay()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(K):
+        append_graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    append_ms = start.elapsed_time(end) / K
+    append_bytes = n_chunks * 2 * 2 * PF_B * PF_C * PF_HKV * D * 2
+    append_bw = append_bytes / (append_ms * 1e-3)
     result = {
         "metric": "chunked prefill tok/s at B=8, 16384 tokens in chunks of 512, GQA 32/8 hd128; "
                   "attention MFMA utilisation",
@@ -302,6 +332,10 @@ def bench_prefill(args):
                      "peak_source": peak_src,
                      "unit": "TFLOP/s", "frac": round(achieved / flops_peak, 4),
                      "traffic": None, "ms_per_pass": round(attn_ms, 4), "flops_per_pass": flops},
+        "append": {"kernel": "kv_append_kernel (K/V copy of the 32 chunks)", "bound": "hbm",
+                   "achieved": round(append_bw / 1e9, 1), "peak": bw_peak / 1e9, "unit": "GB/s",
+                   "frac": round(append_bw / bw_peak, 4), "ms_per_pass": round(append_ms, 4),
+                   "bytes_per_pass": append_bytes},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_prefill_baseline(q, k, v)

@@ -50,6 +50,12 @@ APPEND_CASES = [
     ([0, 100, 37], 64, 2, 64, 200),
     ([2, 9], 3, 2, 16, 16),
     ([1, 0, 4], 2, 1, 16, 8),  # 32-byte rows of bf16: the 16-byte path; fp32 too
+    # Chunk-sized copies: whole 1024-unit blocks plus a tail, token runs of 48 units (a division,
+    # not a shift) and of 32 units (a shift), blocks that straddle tokens.
+    ([0, 300, 1000], 512, 3, 128, 1600),
+    ([5, 1], 700, 2, 128, 800),
+    ([3, 0], 37, 1, 6, 64),  # 12-byte runs of bf16: the 4-byte path (24-byte fp32 runs too)
+    ([2, 9], 33, 1, 5, 64),  # 10-byte runs of bf16: the 2-byte path (20-byte fp32: 4-byte)
 ]
 
 
@@ -82,6 +88,27 @@ def test_append_leaves_rows_past_the_cache_untouched():
     assert np.array_equal(got[1, :15], bits(c["k_cache"])[1, :15])
     assert np.array_equal(got[1, 15], bits(c["k"])[1, 0])  # position 15 fits, 16 does not
     assert np.array_equal(got[0, 3:5], bits(c["k"])[0])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_append_of_a_long_chunk_drops_only_the_positions_past_the_cache(dtype):
+    # Row 1's chunk runs 112 positions past the cache: blocks wholly inside, straddling and wholly
+    # past the end all occur; the rows that fit are copied, nothing else changes.
+    seqlens, T_new, H_kv, D, T_max = [100, 600, 0], 512, 4, 128, 1000
+    _note("append overflow", dtype, seqlens, T_new, H_kv, D, T_max)
+    c = make_case(seqlens, T_new, H_kv, H_kv, D, T_max, dtype, seed=14)
+    g = _gpu(c)
+    lib = _ext.lib()
+    _ext.check(lib.mcamd_kv_append(g["k"].data_ptr(), g["v"].data_ptr(), g["k_cache"].data_ptr(),
+                                   g["v_cache"].data_ptr(), g["cache_seqlens"].data_ptr(),
+                                   len(seqlens), T_new, H_kv, D, T_max, g["k_cache"].stride(0),
+                                   _ext.dtype_code(dtype), _ext.stream_handle(DEV)), "append")
+    for b, p in enumerate(seqlens):
+        fit = min(T_new, T_max - p)
+        ek, ev = ko.append(bits(c["k_cache"])[b:b + 1], bits(c["v_cache"])[b:b + 1],
+                           bits(c["k"])[b:b + 1, :fit], bits(c["v"])[b:b + 1, :fit], [p])
+        assert np.array_equal(bits(g["k_cache"])[b:b + 1], ek), f"row {b}"
+        assert np.array_equal(bits(g["v_cache"])[b:b + 1], ev), f"row {b}"
 
 
 # --- replication --------------------------------------------------------------------------------
