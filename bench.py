@@ -4,8 +4,9 @@
 Workload: batch 32, 16 query / 4 KV heads, head_dim 128, bf16; per-row cache lengths drawn
 uniformly from [512, 8192] (seed 0); K/V cache, q and new k/v are N(0, 1). One step appends one
 token per row at its own position and runs single-token attention over the whole cache
-(``flash_attn_with_kvcache``), then advances the positions (``KVCache.advance``). Inputs are
-resident in HBM before timing starts; the K timed steps run as one HIP graph replay.
+(``flash_attn_with_kvcache``), then advances the positions (``KVCache.advance``; folded into the
+operator's last kernel with ``advance=1`` unless --separate-advance). Inputs are resident in HBM
+before timing starts; the K timed steps run as one HIP graph replay.
 
 Prints one JSON line: tokens/s (32 tokens per step), the roofline of the decode attention
 (algorithmic bytes over its event-timed duration against 8 TB/s), and the reference's CPU
@@ -82,6 +83,10 @@ def parse_args():
                          "KV-sharing stack at B=16, context 4096; sample: a 32-layer 4096-wide "
                          "model prefills one 2048-token prompt, replicates it to 64 rows and "
                          "samples 512 tokens per row at temperature 1")
+    ap.add_argument("--separate-advance", action="store_true",
+                    help="decode and mixed workloads: advance the positions with KVCache.advance "
+                         "after the step's last operator call (one more launch) instead of inside "
+                         "that call (flash_attn_with_kvcache(..., advance=1))")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain device copy of COPY_BYTES, ten times (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -463,7 +468,8 @@ def bench_mixed(args):
     1024; even layers produce K/V into slot i // 2, odd layers read slot (i - 1) // 2 (and
     rewrite the producer's token there, as the reference's consumer call does). B = 16 rows at
     position 4096 + step, H = 12, H_kv = 4, head_dim 128, bf16. One step = 24 operator calls plus
-    the cache advance, replayed from a HIP graph."""
+    the cache advance (inside the last call unless --separate-advance), replayed from a HIP
+    graph."""
     import torch
     from modelcore_amd import stats
     from modelcore_amd.cache import KVCache
@@ -485,14 +491,21 @@ def bench_mixed(args):
     vs = torch.randn(n, n_slots, MX_B, 1, MX_HKV, D, generator=g, device=dev).to(torch.bfloat16)
     windows = [-1 if i % 4 == 3 else MX_WIN for i in range(MX_LAYERS)]
 
+    fold = not args.separate_advance
+
     def step(s):
         for i in range(MX_LAYERS):
             slot = i // 2
             kc, vc = cache.get_slot_cache(slot)
+            last = i == MX_LAYERS - 1
             flash_attn.flash_attn_with_kvcache(qs[s, i], kc, vc, k=ks[s, slot], v=vs[s, slot],
                                                cache_seqlens=cache.cache_seqlens, causal=True,
-                                               window_size=(windows[i], 0))
-        cache.advance(1)
+                                               window_size=(windows[i], 0),
+                                               advance=1 if fold and last else 0)
+        if fold:
+            cache.note_device_advance(1)
+        else:
+            cache.advance(1)
 
     for s in range(W):
         step(s)
@@ -501,6 +514,11 @@ def bench_mixed(args):
     with torch.cuda.graph(graph):
         for s in range(K):
             step(W + s)
+    # One untimed replay (a graph's first launch also uploads it), then the positions set back:
+    # the timed replay rewrites the same new tokens at the same positions.
+    graph.replay()
+    torch.cuda.synchronize()
+    cache.cache_seqlens.fill_(MX_P + W)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     graph.replay()
@@ -524,7 +542,9 @@ def bench_mixed(args):
         "config": {"workload": "KV path of one decode step of a 24-layer stack (18 layers window "
                                "1024, 6 global; odd layers share the previous layer's slot), B=16, "
                                "positions 4096+", "layers": MX_LAYERS, "batch": MX_B,
-                   "n_head": MX_H, "n_kv_head": MX_HKV, "head_dim": D, "timing": "hip_graph"},
+                   "n_head": MX_H, "n_kv_head": MX_HKV, "head_dim": D, "timing": "hip_graph",
+                   "advance": "in the last call's merge pass (advance=1)" if fold
+                              else "KVCache.advance launch"},
         "roofline": {"kernel": "decode_fused_kernel + decode_merge_kernel (24 calls per step)",
                      "bound": "hbm", "achieved": round(gbps, 1), "peak": hbm_peak / 1e9,
                      "peak_source": peak_src, "unit": "GB/s",
@@ -811,8 +831,12 @@ def main():
     def step(i):
         y = flash_attn.flash_attn_with_kvcache(qd[i], k_slot, v_slot, k=kd[i], v=vd[i],
                                                cache_seqlens=cache.cache_seqlens, causal=True,
-                                               window_size=(-1, 0))
-        cache.advance(1)
+                                               window_size=(-1, 0),
+                                               advance=0 if args.separate_advance else 1)
+        if args.separate_advance:
+            cache.advance(1)
+        else:
+            cache.note_device_advance(1)
         return y
 
     log("warm-up")
@@ -829,6 +853,12 @@ def main():
             for i in range(K):
                 step(W + i)
         run = graph.replay
+        # One untimed replay: a graph's first launch also uploads it (~2 us per step more than
+        # later replays, measured). The positions are then set back; the timed replay rewrites the
+        # same new tokens at the same positions, so it computes exactly what it would have.
+        graph.replay()
+        torch.cuda.synchronize()
+        cache.cache_seqlens.copy_((seqlens + W).to(dev))
 
     log(f"timing {K} steps ({'eager' if args.eager else 'one graph replay'})")
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -915,10 +945,13 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "decode microbench: append 1 token per row + single-token attention over "
-                        "the KV cache, B=32, GQA 16q/4kv, head_dim 128, lengths U[512,8192] seed 0",
+                        "the KV cache + position advance, B=32, GQA 16q/4kv, head_dim 128, "
+                        "lengths U[512,8192] seed 0",
             "batch": B, "n_head": H, "n_kv_head": H_KV, "head_dim": D,
             "max_cache_len": t_alloc, "mean_len": round(sum(base) / B + W + K / 2, 1),
             "timing": "eager" if args.eager else "hip_graph",
+            "advance": "KVCache.advance launch" if args.separate_advance
+                       else "in the operator's merge pass (advance=1)",
         },
         "kv_path_gbps": round(step_gbps, 1),
         "kv_path_pct_peak": round(100 * step_gbps * 1e9 / hbm_peak, 2),

@@ -103,6 +103,26 @@ int mcamd_flash_attn_with_kvcache(const void *q, const void *k, const void *v,
                                   void *stream);
 
 /*
+ * mcamd_flash_attn_with_kvcache followed by the step's position advance: once the call has read
+ * cache_seqlens, cache_seqlens[b] += advance for every row b (rows outside the cache included),
+ * on the device, in stream order. For t_new == 1 with bf16 and head_dim 128 the add runs in the
+ * operator's own last pass (the merge, which does not read the positions), so the step needs no
+ * launch of its own for it; the other paths add one small kernel. advance == 0 is exactly
+ * mcamd_flash_attn_with_kvcache. Outputs and cache contents are bit-identical to that call
+ * followed by the separate advance.
+ * Replaces flash_attn_with_kvcache followed by KVCache.advance(advance) in a decode step
+ * (modelcore/kernels/flash_attn.py:306-366, then modelcore/model.py:99-100 ->
+ * modelcore/cache.py:62-73).
+ */
+int mcamd_flash_attn_with_kvcache_advance(const void *q, const void *k, const void *v,
+                                          void *k_cache, void *v_cache, int32_t *cache_seqlens,
+                                          void *out, int64_t batch, int64_t t_new,
+                                          int64_t n_head, int64_t n_kv_head, int64_t head_dim,
+                                          int64_t t_max, int64_t cache_batch_stride,
+                                          int64_t window, int causal, int dtype, int32_t advance,
+                                          void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * mcamd_flash_attn_with_kvcache without the workspace arguments, for callers that cannot allocate
  * device memory (code under graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * It has no counterpart in the reference. Its scratch is a static device array of

@@ -64,6 +64,12 @@ class KVCache:
         """Advance every row by num_tokens. Keeps ragged rows' differences unchanged, which is all
         raggedness is (modelcore/cache.py:62-73)."""
         self.cache_seqlens += num_tokens
+        self.note_device_advance(num_tokens)
+
+    def note_device_advance(self, num_tokens):
+        """Move the host mirror of the positions after an operator call that already advanced
+        cache_seqlens on the device (flash_attn_with_kvcache(..., advance=num_tokens)): the two
+        together are advance(num_tokens)."""
         if self._pos_uniform is not None:
             self._pos_uniform += num_tokens
 

@@ -47,7 +47,7 @@ int check_attn_shapes(const AttnArgs &a, bool need_workspace) {
 
 using namespace mcamd;
 
-extern "C" int mcamd_abi_version(void) { return 5; }
+extern "C" int mcamd_abi_version(void) { return 6; }
 
 extern "C" const char *mcamd_last_error(void) { return g_last_error.c_str(); }
 
@@ -91,6 +91,46 @@ extern "C" int mcamd_prefill_attention(const void *q, const void *k_cache, const
   return launch_prefill(a);
 }
 
+namespace {
+
+// The cached-attention operator: append, then decode (t_new == 1) or chunked prefill; with
+// `advance` != 0 the positions then move on by that much (the decode step's cache advance).
+int kvcache_operator(const void *q, const void *k, const void *v, void *k_cache, void *v_cache,
+                     const int32_t *cache_seqlens, int32_t *advance_seqlens, int advance,
+                     void *out, int64_t batch, int64_t t_new, int64_t n_head, int64_t n_kv_head,
+                     int64_t head_dim, int64_t t_max, int64_t cache_batch_stride, int64_t window,
+                     int dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+  if ((k == nullptr) != (v == nullptr))
+    return fail(MCAMD_EINVAL, "flash_attn_with_kvcache: pass both k and v, or neither");
+  AttnArgs a{q,     k,     v,      k_cache, v_cache,  cache_seqlens, out,
+             batch, t_new, n_head, n_kv_head, head_dim, t_max,       cache_batch_stride,
+             window, dtype, workspace, workspace_bytes, stream};
+  int st = check_attn_shapes(a, t_new == 1);
+  if (st != MCAMD_OK) return st;
+  if (batch == 0) {
+    clear_error();
+    return MCAMD_OK;
+  }
+  if (t_new == 0) return launch_advance(advance_seqlens, batch, advance, stream);
+  if (t_new == 1) {  // appends k/v itself, and advances the positions in its last pass
+    a.advance_seqlens = advance ? advance_seqlens : nullptr;
+    a.advance = advance;
+    return launch_decode(a);
+  }
+  if (k) {
+    AppendArgs ap{k,       v,        k_cache, v_cache, cache_seqlens,      batch, t_new,
+                  n_kv_head, head_dim, t_max, cache_batch_stride, dtype, stream};
+    st = launch_append(ap);
+    if (st != MCAMD_OK) return st;
+  }
+  a.k_new = a.v_new = nullptr;
+  st = launch_prefill(a);
+  if (st != MCAMD_OK) return st;
+  return launch_advance(advance_seqlens, batch, advance, stream);
+}
+
+}  // namespace
+
 extern "C" int mcamd_flash_attn_with_kvcache(const void *q, const void *k, const void *v,
                                              void *k_cache, void *v_cache,
                                              const int32_t *cache_seqlens, void *out,
@@ -100,24 +140,19 @@ extern "C" int mcamd_flash_attn_with_kvcache(const void *q, const void *k, const
                                              int causal, int dtype, void *workspace,
                                              size_t workspace_bytes, void *stream) {
   (void)causal;
-  if ((k == nullptr) != (v == nullptr))
-    return fail(MCAMD_EINVAL, "flash_attn_with_kvcache: pass both k and v, or neither");
-  AttnArgs a{q,     k,     v,      k_cache, v_cache,  cache_seqlens, out,
-             batch, t_new, n_head, n_kv_head, head_dim, t_max,       cache_batch_stride,
-             window, dtype, workspace, workspace_bytes, as_stream(stream)};
-  int st = check_attn_shapes(a, t_new == 1);
-  if (st != MCAMD_OK) return st;
-  if (batch == 0 || t_new == 0) {
-    clear_error();
-    return MCAMD_OK;
-  }
-  if (t_new == 1) return launch_decode(a);  // appends k/v itself
-  if (k) {
-    AppendArgs ap{k,       v,        k_cache, v_cache, cache_seqlens,      batch, t_new,
-                  n_kv_head, head_dim, t_max, cache_batch_stride, dtype, as_stream(stream)};
-    st = launch_append(ap);
-    if (st != MCAMD_OK) return st;
-  }
-  a.k_new = a.v_new = nullptr;
-  return launch_prefill(a);
+  return kvcache_operator(q, k, v, k_cache, v_cache, cache_seqlens, nullptr, 0, out, batch, t_new,
+                          n_head, n_kv_head, head_dim, t_max, cache_batch_stride, window, dtype,
+                          workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int mcamd_flash_attn_with_kvcache_advance(
+    const void *q, const void *k, const void *v, void *k_cache, void *v_cache,
+    int32_t *cache_seqlens, void *out, int64_t batch, int64_t t_new, int64_t n_head,
+    int64_t n_kv_head, int64_t head_dim, int64_t t_max, int64_t cache_batch_stride,
+    int64_t window, int causal, int dtype, int32_t advance, void *workspace,
+    size_t workspace_bytes, void *stream) {
+  (void)causal;
+  return kvcache_operator(q, k, v, k_cache, v_cache, cache_seqlens, cache_seqlens, advance, out,
+                          batch, t_new, n_head, n_kv_head, head_dim, t_max, cache_batch_stride,
+                          window, dtype, workspace, workspace_bytes, as_stream(stream));
 }

@@ -102,7 +102,9 @@ struct FusedParams {
   uint16_t *out;
   float *part;  // [B * n_units * kBucket][kPart]: segment j < kBucket of unit u at u * kBucket + j
   float *over;  // [kMaxGroups + B * n_units][kPart]: segments j >= kBucket, slot = group + unit
-  int2 *desc;   // [B * n_units]: (first workgroup, segments) of each unit that has keys
+  int2 *desc;   // [B * n_units]: (first workgroup, segments) of each unit; (0, 0): no keys
+  int32_t *adv_seqlens;  // the merge pass adds `advance` to every row's position (0: it does not)
+  int advance;
   int B, H, H_kv, G, n_hc, n_kg, n_units, T_max, window, n_groups;
   int scan32;  // B <= 64 and every sum of row slot counts fits in 31 bits
   int64_t cache_b;
@@ -325,11 +327,15 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(FusedParams P) {
   const int r = lane >> 4;  // KV head within the unit's group of four
   const int c = lane & 15;  // 16-byte column of the head row
 
-  // Rows outside the cache: NaN output, written by workgroup b % n_groups.
+  // Rows outside the cache: NaN output and a descriptor of no segments for each of their units
+  // (so the merge pass need not read cache_seqlens), written by workgroup b % n_groups.
   for (int b = g; b < P.B; b += P.n_groups) {
     int lo;
-    if (row_keys(P, b, lo) == 0)
+    if (row_keys(P, b, lo) == 0) {
       for (int i = threadIdx.x; i < P.H * D; i += 64 * NW) P.out[int64_t(b) * P.H * D + i] = 0x7fc0;
+      for (int u = threadIdx.x; u < P.n_units; u += 64 * NW)
+        P.desc[int64_t(b) * P.n_units + u] = make_int2(0, 0);
+    }
   }
   // NG <= T active workgroups: every range [g*T/NG, (g+1)*T/NG) is then non-empty, so the
   // workgroups holding a unit's keys are exactly those from its first key's owner to its last
@@ -601,10 +607,12 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(FusedParams P) {
 }
 
 // Merge pass with one wave per (unit, query head): lane l combines dims 2l, 2l+1 of that head
-// over the unit's segments. The loads of the unit's first SPEC bucket slots are issued with those
-// of its descriptor and row length, before the segment count is known (one memory round trip for
-// units of up to SPEC segments; slots past the count hold other calls' data and are ignored);
-// later segments follow BATCH at a time.
+// over the unit's segments. The loads of the unit's first SPEC bucket slots are issued with that
+// of its descriptor, before the segment count is known (one memory round trip for units of up to
+// SPEC segments; slots past the count hold other calls' data and are ignored); later segments
+// follow BATCH at a time. The pass does not read cache_seqlens (the descriptors carry all it
+// needs), so it can also advance the positions: the wave of each row's first unit and head adds
+// `advance` to the row's entry.
 template <int SPEC>
 __global__ __launch_bounds__(64) void decode_merge_kernel(FusedParams P) {
   constexpr int BATCH = 8;
@@ -617,16 +625,15 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(FusedParams P) {
   const int hc = unit - kg * P.n_hc;
   const int kvh = kg * KG + hr / GM;
   const int hh = hr % GM;
+  if (P.advance != 0 && unit == 0 && hr == 0 && lane == 0) P.adv_seqlens[b] += P.advance;
   if (kvh >= P.H_kv || hh >= min(GM, P.G - hc * GM)) return;
   const float *bucket = P.part + int64_t(ug) * kBucket * kPart;
   auto seg_at = [&](int j, int g_first) {
     return j < kBucket ? bucket + int64_t(j) * kPart : P.over + int64_t(g_first + j + ug) * kPart;
   };
-  // The unit's (first workgroup, segments), published by the streaming pass; a row outside the
-  // cache has no keys and no descriptor (its NaN output is written), so it is checked too.
+  // The unit's (first workgroup, segments), published by the streaming pass: no segments for a
+  // row outside the cache (its NaN output is written), one for a unit written directly.
   const int2 d = P.desc[ug];
-  int lo;
-  const int nk = row_keys(P, b, lo);
   float2 ml[SPEC], v[SPEC];
 #pragma unroll
   for (int k = 0; k < SPEC; ++k) {
@@ -634,9 +641,8 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(FusedParams P) {
     ml[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * hr);
     v[k] = *reinterpret_cast<const float2 *>(ps + hr * D + 2 * lane);
   }
-  if (nk == 0) return;
   const int g_first = d.x, nseg = d.y;
-  if (nseg == 1) return;  // written directly by the streaming pass
+  if (nseg <= 1) return;  // no keys, or written directly by the streaming pass
   float M = -INFINITY, L = 0.f, t0 = 0.f, t1 = 0.f;
   auto add = [&](float2 mlk, float2 vk, bool valid) {
     const float mk = valid ? mlk.x : -INFINITY;
@@ -708,6 +714,8 @@ int launch_decode_fused(const AttnArgs &a) {
   P.k_cache = static_cast<uint16_t *>(const_cast<void *>(a.k_cache));
   P.v_cache = static_cast<uint16_t *>(const_cast<void *>(a.v_cache));
   P.seqlens = a.seqlens;
+  P.adv_seqlens = a.advance_seqlens;
+  P.advance = a.advance_seqlens ? a.advance : 0;
   P.out = static_cast<uint16_t *>(a.out);
   P.B = int(a.batch);
   P.H = int(a.n_head);

@@ -336,8 +336,10 @@ int launch_decode(const AttnArgs &a) {
   P.k_new = P.v_new = nullptr;  // appended above
   P.part_o = static_cast<float *>(a.workspace);
   P.part_ml = P.part_o + floats_o;
-  if (a.dtype == MCAMD_BF16) return dispatch_d<bf16>(P, int(a.batch), a.stream);
-  return dispatch_d<float>(P, int(a.batch), a.stream);
+  st = a.dtype == MCAMD_BF16 ? dispatch_d<bf16>(P, int(a.batch), a.stream)
+                             : dispatch_d<float>(P, int(a.batch), a.stream);
+  if (st != MCAMD_OK || !a.advance_seqlens) return st;
+  return launch_advance(a.advance_seqlens, a.batch, a.advance, a.stream);
 }
 
 }  // namespace mcamd

@@ -16,6 +16,9 @@ struct AppendArgs {
 };
 int launch_append(const AppendArgs &a);
 
+// seqlens[b] += advance for b < batch, one small kernel on `stream`.
+int launch_advance(int32_t *seqlens, int64_t batch, int advance, hipStream_t stream);
+
 struct AttnArgs {
   const void *q;
   const void *k_new, *v_new;  // decode only: the token at position cache_seqlens[b] is read from
@@ -28,6 +31,11 @@ struct AttnArgs {
   void *workspace;
   size_t workspace_bytes;
   hipStream_t stream;
+  // After the call has read the positions, cache_seqlens[b] += advance for every row (the
+  // position advance of a decode step). The bf16 / head_dim 128 decode does it in its merge pass;
+  // the other paths launch launch_advance after their kernels. advance 0: positions only read.
+  int32_t *advance_seqlens = nullptr;
+  int advance = 0;
 };
 int launch_decode(const AttnArgs &a);
 int launch_prefill(const AttnArgs &a);

@@ -109,7 +109,25 @@ int run(const AppendArgs &a, int64_t row_bytes) {
   return launch_status("kv_append");
 }
 
+// Position advance of a decode step (modelcore/cache.py:62-73, cache_seqlens += num_tokens), for
+// the operator paths whose kernels have no later pass to fold it into.
+__global__ __launch_bounds__(256) void advance_kernel(int32_t *seqlens, int batch, int by) {
+  for (int b = blockIdx.x * 256 + threadIdx.x; b < batch; b += gridDim.x * 256) seqlens[b] += by;
+}
+
 }  // namespace
+
+int launch_advance(int32_t *seqlens, int64_t batch, int advance, hipStream_t stream) {
+  if (batch <= 0 || advance == 0) {
+    clear_error();
+    return MCAMD_OK;
+  }
+  if (!seqlens) return fail(MCAMD_EINVAL, "advance: null cache_seqlens");
+  const int blocks = int(std::min<int64_t>((batch + 255) / 256, 256));
+  hipLaunchKernelGGL(advance_kernel, dim3(blocks), dim3(256), 0, stream, seqlens, int(batch),
+                     advance);
+  return launch_status("advance");
+}
 
 int launch_append(const AppendArgs &a) {
   if (a.dtype != MCAMD_F32 && a.dtype != MCAMD_BF16)

@@ -9,7 +9,8 @@ Usage is the reference's (modelcore/kernels/flash_attn.py:7-14)::
                                            causal=True, window_size=(window, 0))
 
 Semantics are the reference fallback's (modelcore/kernels/flash_attn.py:330-366): the new
-tokens' K/V are written in place at ``cache_seqlens`` (which is read, never advanced), and query
+tokens' K/V are written in place at ``cache_seqlens`` (which is read, and advanced only when the
+call asks for it with ``advance``), and query
 t of row b, at position p = cache_seqlens[b] + t, attends keys col <= p with p - col <=
 window_size[0] when that is >= 0. GQA maps query head h to KV head h // (H // H_kv). The softmax
 scale is 1/sqrt(D). Uniform and ragged ``cache_seqlens`` run the same kernels (the reference's
@@ -131,7 +132,7 @@ def _window(window_size):
 # Public API: same interface as the reference (modelcore/kernels/flash_attn.py:270-366).
 # -----------------------------------------------------------------------------------------------
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
-                            causal=False, window_size=(-1, -1)):
+                            causal=False, window_size=(-1, -1), *, advance=0):
     """Attention with KV cache for inference (modelcore/kernels/flash_attn.py:306-366).
 
     Args:
@@ -142,6 +143,13 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
         causal: accepted for signature parity; attention is always causal, as in the reference
             fallback
         window_size: (left, right); left = -1 means unlimited
+        advance: extension, no counterpart in the reference operator. Non-zero: once the call has
+            read cache_seqlens, add this to every row's entry on the device -- the
+            KVCache.advance(advance) that follows the last layer's call in a decode step
+            (modelcore/model.py:99-100, modelcore/cache.py:62-73). The single-token bf16 /
+            head_dim 128 path does it in its last kernel, so the step saves that launch. The host
+            side of a KVCache then moves with KVCache.note_device_advance. 0 (default): the
+            reference behaviour, cache_seqlens only read.
 
     Returns:
         (B, T_new, H, D) tensor in q's dtype.
@@ -166,6 +174,10 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
             raise TypeError(f"{name} is {t.dtype}, q is {dt}")
     code = _ext.dtype_code(dt)
     seqlens = _check_seqlens(cache_seqlens, B, q.device)
+    advance = int(advance)
+    if advance and seqlens.data_ptr() != cache_seqlens.data_ptr():
+        raise ValueError("advance needs cache_seqlens itself to be contiguous (it is updated in "
+                         "place)")
     if CHECK_POSITIONS and B > 0:
         _check_positions(seqlens, T_new, T_max)
     q = q.contiguous()
@@ -176,13 +188,16 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
     w = _window(window_size)
     ws_bytes = lib.mcamd_attn_workspace_bytes(B, T_new, H, H_kv, D, T_max, w)
     ws = _ext.workspace(q.device, ws_bytes)
-    st = lib.mcamd_flash_attn_with_kvcache(
-        q.data_ptr(), k.data_ptr() if k is not None else None,
-        v.data_ptr() if v is not None else None, k_cache.data_ptr(), v_cache.data_ptr(),
-        seqlens.data_ptr(), out.data_ptr(), B, T_new, H, H_kv, D, T_max, k_cache.stride(0), w,
-        int(bool(causal)), code, ws.data_ptr() if ws is not None else None,
-        ws.numel() if ws is not None else 0,
-        _ext.stream_handle(q.device))
+    args = (q.data_ptr(), k.data_ptr() if k is not None else None,
+            v.data_ptr() if v is not None else None, k_cache.data_ptr(), v_cache.data_ptr(),
+            seqlens.data_ptr(), out.data_ptr(), B, T_new, H, H_kv, D, T_max, k_cache.stride(0), w,
+            int(bool(causal)), code)
+    ws_args = (ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+               _ext.stream_handle(q.device))
+    if advance:
+        st = lib.mcamd_flash_attn_with_kvcache_advance(*args, advance, *ws_args)
+    else:
+        st = lib.mcamd_flash_attn_with_kvcache(*args, *ws_args)
     _ext.check(st, "flash_attn_with_kvcache")
     return out
 
