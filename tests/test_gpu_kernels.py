@@ -115,7 +115,10 @@ def test_append_of_a_long_chunk_drops_only_the_positions_past_the_cache(dtype):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("slots,rows,P,H_kv,D", [(2, 4, 7, 2, 8), (3, 64, 129, 8, 128),
-                                                 (1, 5, 33, 1, 16)])
+                                                 (1, 5, 33, 1, 16),
+                                                 # whole 4096-unit blocks plus a tail: 16-byte
+                                                 # units, then 4-byte units (20-byte bf16 rows)
+                                                 (2, 3, 1000, 3, 20), (2, 5, 1001, 1, 10)])
 def test_prefill_replicates_bit_exactly(dtype, slots, rows, P, H_kv, D):
     _note("replicate", dtype, slots, rows, P, H_kv, D)
     g = gen(13)
