@@ -90,6 +90,7 @@ constexpr int kBucket = MCAMD_DECODE_BUCKET;
 // Bucket slots the merge loads before the count is known, at most; a launch loads fewer (4 or 8)
 // when its units average fewer segments (see launch_decode_fused).
 constexpr int kSpec = MCAMD_DECODE_SPEC;
+constexpr int64_t kTemporalLimit = int64_t(64) << 20;  // bytes of K/V: see launch_decode_fused
 static_assert(kSpec <= kBucket, "speculative merge loads stay inside the unit's bucket");
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -319,6 +320,9 @@ __device__ __forceinline__ int xcd_major(int id, int n) {
   return x * (n / 8) + min(x, n % 8) + i;
 }
 
+// NT: K/V loads non-temporal (calls too large to stay in the memory-side cache) or with the
+// default policy (small calls, whose K/V a KV-sharing layer may read again right after).
+template <bool NT>
 __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(FusedParams P) {
   __shared__ WaveAcc s_acc[NW];
   const int lane = threadIdx.x & 63;
@@ -394,8 +398,13 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(FusedParams P) {
         const bool is_new = fuse_new && t == pos;
         const uint16_t *kp = is_new ? P.k_new + new_off : kbase + int64_t(t) * tok_stride;
         const uint16_t *vp = is_new ? P.v_new + new_off : vbase + int64_t(t) * tok_stride;
-        Tl.k[j] = load_stream(kp);
-        Tl.v[j] = load_stream(vp);
+        if constexpr (NT) {
+          Tl.k[j] = load_stream(kp);
+          Tl.v[j] = load_stream(vp);
+        } else {
+          Tl.k[j] = *reinterpret_cast<const uint4 *>(kp);
+          Tl.v[j] = *reinterpret_cast<const uint4 *>(vp);
+        }
       }
     };
 
@@ -742,7 +751,17 @@ int launch_decode_fused(const AttnArgs &a) {
   P.part = reinterpret_cast<float *>(ws);
   P.over = P.part + units * kBucket * kPart;
   P.desc = reinterpret_cast<int2 *>(P.over + (kMaxGroups + units) * kPart);
-  hipLaunchKernelGGL(decode_fused_kernel, dim3(unsigned(groups)), dim3(64 * NW), 0, a.stream, P);
+  // K/V bytes the call can read (every row at its longest span). A call that fits in a quarter
+  // of the 256 MB memory-side cache loads them with the default policy, so a KV-sharing layer
+  // that reads the same slot next finds them there (measured on the 24-layer mixed-window stack:
+  // 0.413 -> 0.393 ms per step; the same for its global calls too: 0.412, no gain). Larger calls
+  // stream non-temporal: allocating lines that no later read finds costs bandwidth (the decode
+  // microbench's call with the default policy, alternating two caches: 57.3 against 49.8 us).
+  const int64_t kv_bytes = int64_t(a.batch) * span * a.n_kv_head * D * 2 * 2;
+  if (kv_bytes <= kTemporalLimit)
+    hipLaunchKernelGGL(decode_fused_kernel<false>, dim3(unsigned(groups)), dim3(64 * NW), 0, a.stream, P);
+  else
+    hipLaunchKernelGGL(decode_fused_kernel<true>, dim3(unsigned(groups)), dim3(64 * NW), 0, a.stream, P);
   int st = launch_status("decode_fused");
   if (st != MCAMD_OK) return st;
   const dim3 merge_grid(unsigned(a.batch * P.n_units * KG * GM));
