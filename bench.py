@@ -140,6 +140,28 @@ def measured_traffic(bytes_now):
                                                      f"scaled by its ratio {traffic / algo:.4f}")
 
 
+APPEND_TRAFFIC_FILE = "profiles/kv_append_b8_c512_hkv8_hd128_traffic.md"
+
+
+def append_traffic(bytes_now):
+    """(HBM bytes per append launch, where the figure comes from) from the committed counter
+    profile of the prefill workload's append, when it was measured for launches of these
+    algorithmic bytes; (None, reason) otherwise."""
+    import re
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), APPEND_TRAFFIC_FILE)
+    try:
+        with open(path) as f:
+            text = f.read()
+    except OSError:
+        return None, f"{APPEND_TRAFFIC_FILE} missing"
+    t = re.search(r"^append_traffic_bytes_per_launch:\s*(\d+)", text, re.M)
+    a = re.search(r"^append_algorithmic_bytes_per_launch:\s*(\d+)", text, re.M)
+    if not (t and a) or int(a.group(1)) != bytes_now:
+        return None, f"{APPEND_TRAFFIC_FILE} holds no figure for launches of {bytes_now} bytes"
+    return int(t.group(1)), (f"{APPEND_TRAFFIC_FILE}: rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE "
+                             f"(copy-calibrated), mean over 128 launches of this workload")
+
+
 def _counter_rows(path):
     import csv
     with open(path) as f:
@@ -320,6 +342,7 @@ def bench_prefill(args):
     append_ms = start.elapsed_time(end) / K
     append_bytes = n_chunks * 2 * 2 * PF_B * PF_C * PF_HKV * D * 2
     append_bw = append_bytes / (append_ms * 1e-3)
+    append_traffic_launch, append_traffic_src = append_traffic(append_bytes // n_chunks)
     result = {
         "metric": "chunked prefill tok/s at B=8, 16384 tokens in chunks of 512, GQA 32/8 hd128; "
                   "attention MFMA utilisation",
@@ -340,7 +363,9 @@ def bench_prefill(args):
         "append": {"kernel": "kv_append_kernel (K/V copy of the 32 chunks)", "bound": "hbm",
                    "achieved": round(append_bw / 1e9, 1), "peak": bw_peak / 1e9, "unit": "GB/s",
                    "frac": round(append_bw / bw_peak, 4), "ms_per_pass": round(append_ms, 4),
-                   "bytes_per_pass": append_bytes},
+                   "bytes_per_pass": append_bytes, "traffic": append_traffic_launch,
+                   "traffic_source": append_traffic_src,
+                   "bytes_per_launch": append_bytes // n_chunks},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_prefill_baseline(q, k, v)
