@@ -87,6 +87,9 @@ def parse_args():
                     help="decode and mixed workloads: advance the positions with KVCache.advance "
                          "after the step's last operator call (one more launch) instead of inside "
                          "that call (flash_attn_with_kvcache(..., advance=1))")
+    ap.add_argument("--no-shared-prefix", action="store_true",
+                    help="sample workload: let every row's attention read its own copy of the "
+                         "replicated prompt's K/V instead of row 0's (KVCache.shared_prefix = 0)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain device copy of COPY_BYTES, ten times (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -692,7 +695,8 @@ def bench_sample(args):
     2048-token prompt (uniform random tokens, seed 0) at batch 1, replicates its cache into 64
     rows (KVCache.prefill), then decodes 512 tokens per row, each drawn on the device at
     temperature 1.0 from a per-row Philox stream (row r seeded r). The first --warmup steps are
-    untimed; the value is rows x timed steps / time."""
+    untimed; the value is rows x timed steps / time. The decode attention reads the replicated
+    prompt's K/V from row 0 for every row (KVCache.shared_prefix) unless --no-shared-prefix."""
     import torch
     from modelcore_amd import stats
     from modelcore_amd.model import ModelManager
@@ -717,6 +721,9 @@ def bench_sample(args):
     end.record()
     torch.cuda.synchronize()
     prefill_ms = start.elapsed_time(end)
+    assert dec.kv_cache.shared_prefix == SM_PROMPT, "KVCache.prefill records the shared prompt"
+    if args.no_shared_prefix:
+        dec.kv_cache.shared_prefix = 0
     sampler = PhiloxSampler(SM_ROWS, dev, base_seed=0)
     graph = not args.eager
     if graph and W == 0:  # capturing runs one real step first
@@ -766,12 +773,18 @@ def bench_sample(args):
                    "decode_gemm": "F.linear" if args.library_gemm else "mcamd_linear_bf16",
                    "residual_step": "torch add + F.rms_norm" if args.separate_residual
                    else "mcamd_residual_rmsnorm",
-                   "prefill_and_replicate_ms": round(prefill_ms, 2)},
+                   "prefill_and_replicate_ms": round(prefill_ms, 2),
+                   "shared_prefix": dec.kv_cache.shared_prefix},
         "roofline": {"kernel": "whole decode step (bf16 weight GEMMs + cached attention of 32 "
                                "layers + sampling)", "bound": "hbm", "achieved": round(gbps, 1),
                      "peak": hbm_peak / 1e9, "peak_source": peak_src, "unit": "GB/s",
                      "frac": round(gbps * 1e9 / hbm_peak, 4), "traffic": None,
-                     "bytes_per_step": int(step_bytes), "weight_bytes": int(weight_bytes)},
+                     "bytes_per_step": int(step_bytes), "weight_bytes": int(weight_bytes),
+                     "kv_bytes_per_step": int(kv),
+                     "kv_note": "every row's K/V counted, as the reference's byte model does; "
+                                "with shared_prefix > 0 the rows read the prompt's K/V from row "
+                                "0, so most of those reads are served by L2 and the memory-side "
+                                "cache rather than HBM"},
     }
     if not args.no_cpu_baseline:
         log("CPU baseline: one decode step of a 1-layer copy of the model on host cores")

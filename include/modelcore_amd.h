@@ -103,24 +103,32 @@ int mcamd_flash_attn_with_kvcache(const void *q, const void *k, const void *v,
                                   void *stream);
 
 /*
- * mcamd_flash_attn_with_kvcache followed by the step's position advance: once the call has read
- * cache_seqlens, cache_seqlens[b] += advance for every row b (rows outside the cache included),
- * on the device, in stream order. For t_new == 1 with bf16 and head_dim 128 the add runs in the
- * operator's own last pass (the merge, which does not read the positions), so the step needs no
- * launch of its own for it; the other paths add one small kernel. advance == 0 is exactly
- * mcamd_flash_attn_with_kvcache. Outputs and cache contents are bit-identical to that call
- * followed by the separate advance.
+ * mcamd_flash_attn_with_kvcache with two extensions of the decode step, each off at 0.
+ *  - advance: once the call has read cache_seqlens, cache_seqlens[b] += advance for every row b
+ *    (rows outside the cache included), on the device, in stream order -- the step's position
+ *    advance. For t_new == 1 with bf16 and head_dim 128 the add runs in the operator's own last
+ *    pass (the merge, which does not read the positions), so the step needs no launch of its own
+ *    for it; the other paths add one small kernel.
+ *  - shared_prefix (0 <= shared_prefix <= t_max): the caller states that every row's K and V at
+ *    positions [0, shared_prefix) are the same as row 0's (rows replicated from one prompt), and
+ *    that every new token lands at or past shared_prefix. For t_new == 1 with bf16 and head_dim
+ *    128 those keys are then read from row 0 for every row -- the same values, so the same
+ *    results -- and the rows' repeated reads of one row's lines are served by the caches instead
+ *    of HBM. Other paths read each row's own copy. A statement that does not hold gives rows
+ *    row 0's keys below shared_prefix.
+ * With both 0 this is exactly mcamd_flash_attn_with_kvcache; otherwise outputs and cache contents
+ * are bit-identical to that call (followed by the separate advance) whenever the statement holds.
  * Replaces flash_attn_with_kvcache followed by KVCache.advance(advance) in a decode step
  * (modelcore/kernels/flash_attn.py:306-366, then modelcore/model.py:99-100 ->
- * modelcore/cache.py:62-73).
+ * modelcore/cache.py:62-73), after KVCache.prefill's replication (modelcore/cache.py:75-90).
  */
-int mcamd_flash_attn_with_kvcache_advance(const void *q, const void *k, const void *v,
-                                          void *k_cache, void *v_cache, int32_t *cache_seqlens,
-                                          void *out, int64_t batch, int64_t t_new,
-                                          int64_t n_head, int64_t n_kv_head, int64_t head_dim,
-                                          int64_t t_max, int64_t cache_batch_stride,
-                                          int64_t window, int causal, int dtype, int32_t advance,
-                                          void *workspace, size_t workspace_bytes, void *stream);
+int mcamd_flash_attn_with_kvcache_ex(const void *q, const void *k, const void *v, void *k_cache,
+                                     void *v_cache, int32_t *cache_seqlens, void *out,
+                                     int64_t batch, int64_t t_new, int64_t n_head,
+                                     int64_t n_kv_head, int64_t head_dim, int64_t t_max,
+                                     int64_t cache_batch_stride, int64_t window, int causal,
+                                     int dtype, int32_t advance, int64_t shared_prefix,
+                                     void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * mcamd_flash_attn_with_kvcache without the workspace arguments, for callers that cannot allocate

@@ -7,6 +7,10 @@ tensors of shape (n_slots, B, T_max, H_kv, D) in the compute dtype, zero-filled 
 ``cache_seqlens`` is the per-row position on the device (int32), and ``_pos_uniform`` its host
 mirror (the shared position, or None once rows are right-ragged).
 
+One attribute is added to the reference's: ``shared_prefix``, the number of leading positions at
+which every row holds the same K/V (after ``prefill`` of one prompt into all rows), which the
+decode operator can exploit (``flash_attn_with_kvcache(..., shared_prefix=...)``).
+
 The copies of ``prefill`` and ``prefill_row`` run the HIP replication kernel
 (``mcamd_kv_replicate``); the appends happen inside the attention operator
 (``modelcore_amd.kernels.flash_attn``). Position bookkeeping (``advance``, ``reset``) stays on
@@ -38,6 +42,10 @@ class KVCache:
         self._pos_uniform = 0
         # Non-KV per-row state (recurrent/smear state); every tensor is (batch, ...).
         self.state = {}
+        # Positions [0, shared_prefix) of every row hold copies of row 0's K/V (prefill() of one
+        # prompt into all rows); the decode operator may then read them from row 0 for every row.
+        # Not in the reference: set by prefill(), cleared by reset() and the per-row prefills.
+        self.shared_prefix = 0
 
     def reset(self):
         """Back to empty. K/V are deliberately not zeroed: a row only ever reads keys at indices
@@ -45,6 +53,7 @@ class KVCache:
         self.cache_seqlens.zero_()
         self.state = {}
         self._pos_uniform = 0
+        self.shared_prefix = 0
 
     def get_pos(self):
         """The single position every row is at; raises on a right-ragged cache."""
@@ -112,6 +121,7 @@ class KVCache:
         self._replicate_from(other, 0, self.batch_size, other_pos)
         self.cache_seqlens.fill_(other_pos)
         self._pos_uniform = other_pos
+        self.shared_prefix = other_pos  # every row (row 0 included) now holds the same prompt
         # Expand any batch=1 extra state to every row.
         for key, value in other.state.items():
             self.state[key] = value.expand(self.batch_size, *([-1] * (value.dim() - 1))).clone()
@@ -137,6 +147,7 @@ class KVCache:
         per_row = [n for n in lengths for _ in range(num_samples)]
         self.cache_seqlens.copy_(torch.tensor(per_row, dtype=torch.int32))
         self._pos_uniform = per_row[0] if len(set(per_row)) == 1 else None
+        self.shared_prefix = lengths[0] if len(lengths) == 1 else 0  # one prompt: all rows alike
 
     def prefill_row(self, row, other):
         """Copy a batch=1 prefilled cache into row `row` only (modelcore/cache.py:92-119); rows
@@ -149,6 +160,7 @@ class KVCache:
         assert other_pos <= self.max_seq_len, f"prompt of {other_pos} tokens exceeds cache length {self.max_seq_len}"
         self._replicate_from(other, row, 1, other_pos)
         self.cache_seqlens[row] = other_pos
+        self.shared_prefix = 0  # rows may now hold different prompts
         # Per-row extra state: a zero buffer per key, shaped from the source, filled row by row.
         for key, value in other.state.items():
             if key not in self.state:

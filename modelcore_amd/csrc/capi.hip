@@ -47,7 +47,7 @@ int check_attn_shapes(const AttnArgs &a, bool need_workspace) {
 
 using namespace mcamd;
 
-extern "C" int mcamd_abi_version(void) { return 6; }
+extern "C" int mcamd_abi_version(void) { return 7; }
 
 extern "C" const char *mcamd_last_error(void) { return g_last_error.c_str(); }
 
@@ -94,12 +94,14 @@ extern "C" int mcamd_prefill_attention(const void *q, const void *k_cache, const
 namespace {
 
 // The cached-attention operator: append, then decode (t_new == 1) or chunked prefill; with
-// `advance` != 0 the positions then move on by that much (the decode step's cache advance).
+// `advance` != 0 the positions then move on by that much (the decode step's cache advance);
+// `shared_prefix` > 0 states that keys [0, shared_prefix) are the same in every row.
 int kvcache_operator(const void *q, const void *k, const void *v, void *k_cache, void *v_cache,
                      const int32_t *cache_seqlens, int32_t *advance_seqlens, int advance,
-                     void *out, int64_t batch, int64_t t_new, int64_t n_head, int64_t n_kv_head,
-                     int64_t head_dim, int64_t t_max, int64_t cache_batch_stride, int64_t window,
-                     int dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+                     int64_t shared_prefix, void *out, int64_t batch, int64_t t_new,
+                     int64_t n_head, int64_t n_kv_head, int64_t head_dim, int64_t t_max,
+                     int64_t cache_batch_stride, int64_t window, int dtype, void *workspace,
+                     size_t workspace_bytes, hipStream_t stream) {
   if ((k == nullptr) != (v == nullptr))
     return fail(MCAMD_EINVAL, "flash_attn_with_kvcache: pass both k and v, or neither");
   AttnArgs a{q,     k,     v,      k_cache, v_cache,  cache_seqlens, out,
@@ -107,6 +109,8 @@ int kvcache_operator(const void *q, const void *k, const void *v, void *k_cache,
              window, dtype, workspace, workspace_bytes, stream};
   int st = check_attn_shapes(a, t_new == 1);
   if (st != MCAMD_OK) return st;
+  if (shared_prefix < 0 || shared_prefix > t_max)
+    return fail(MCAMD_EINVAL, "flash_attn_with_kvcache: shared_prefix outside [0, t_max]");
   if (batch == 0) {
     clear_error();
     return MCAMD_OK;
@@ -115,6 +119,7 @@ int kvcache_operator(const void *q, const void *k, const void *v, void *k_cache,
   if (t_new == 1) {  // appends k/v itself, and advances the positions in its last pass
     a.advance_seqlens = advance ? advance_seqlens : nullptr;
     a.advance = advance;
+    a.shared_prefix = shared_prefix;
     return launch_decode(a);
   }
   if (k) {
@@ -140,19 +145,20 @@ extern "C" int mcamd_flash_attn_with_kvcache(const void *q, const void *k, const
                                              int causal, int dtype, void *workspace,
                                              size_t workspace_bytes, void *stream) {
   (void)causal;
-  return kvcache_operator(q, k, v, k_cache, v_cache, cache_seqlens, nullptr, 0, out, batch, t_new,
-                          n_head, n_kv_head, head_dim, t_max, cache_batch_stride, window, dtype,
-                          workspace, workspace_bytes, as_stream(stream));
+  return kvcache_operator(q, k, v, k_cache, v_cache, cache_seqlens, nullptr, 0, 0, out, batch,
+                          t_new, n_head, n_kv_head, head_dim, t_max, cache_batch_stride, window,
+                          dtype, workspace, workspace_bytes, as_stream(stream));
 }
 
-extern "C" int mcamd_flash_attn_with_kvcache_advance(
+extern "C" int mcamd_flash_attn_with_kvcache_ex(
     const void *q, const void *k, const void *v, void *k_cache, void *v_cache,
     int32_t *cache_seqlens, void *out, int64_t batch, int64_t t_new, int64_t n_head,
     int64_t n_kv_head, int64_t head_dim, int64_t t_max, int64_t cache_batch_stride,
-    int64_t window, int causal, int dtype, int32_t advance, void *workspace,
-    size_t workspace_bytes, void *stream) {
+    int64_t window, int causal, int dtype, int32_t advance, int64_t shared_prefix,
+    void *workspace, size_t workspace_bytes, void *stream) {
   (void)causal;
-  return kvcache_operator(q, k, v, k_cache, v_cache, cache_seqlens, cache_seqlens, advance, out,
-                          batch, t_new, n_head, n_kv_head, head_dim, t_max, cache_batch_stride,
-                          window, dtype, workspace, workspace_bytes, as_stream(stream));
+  return kvcache_operator(q, k, v, k_cache, v_cache, cache_seqlens, cache_seqlens, advance,
+                          shared_prefix, out, batch, t_new, n_head, n_kv_head, head_dim, t_max,
+                          cache_batch_stride, window, dtype, workspace, workspace_bytes,
+                          as_stream(stream));
 }

@@ -40,6 +40,10 @@
 //    segment count), so the merge pass finds the partials without rebuilding the work split.
 //  * Append: the segment that ends at p reads the new token from k/v instead of the cache and
 //    its lanes store it into the cache at p (bit-exact copy; the first query-head group only).
+//  * Shared prefix: when the caller states that every row's keys [0, S) are copies of row 0's
+//    (rows replicated from one prompt), those keys are read from row 0 for every row. The values
+//    are the same, so are the results; the rows' repeated reads of one row's lines are served by
+//    L2 and the memory-side cache instead of HBM.
 #include "kernels.h"
 
 #include <cmath>
@@ -106,6 +110,7 @@ struct FusedParams {
   int2 *desc;   // [B * n_units]: (first workgroup, segments) of each unit; (0, 0): no keys
   int32_t *adv_seqlens;  // the merge pass adds `advance` to every row's position (0: it does not)
   int advance;
+  int shared;  // keys [0, shared) are read from row 0 for every row
   int B, H, H_kv, G, n_hc, n_kg, n_units, T_max, window, n_groups;
   int scan32;  // B <= 64 and every sum of row slot counts fits in 31 bits
   int64_t cache_b;
@@ -387,6 +392,9 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(FusedParams P) {
 
     const uint16_t *kbase = P.k_cache + int64_t(b) * P.cache_b + int64_t(kvh) * D + c * 8;
     const uint16_t *vbase = P.v_cache + int64_t(b) * P.cache_b + int64_t(kvh) * D + c * 8;
+    // Row 0's copy of the keys every row shares (the same bytes as the row's own).
+    const uint16_t *kbase0 = P.k_cache + int64_t(kvh) * D + c * 8;
+    const uint16_t *vbase0 = P.v_cache + int64_t(kvh) * D + c * 8;
     const int64_t new_off = (int64_t(b) * P.H_kv + kvh) * D + c * 8;
 
     // Loads are unconditional (keys past the segment re-read its last key and are masked), so
@@ -396,8 +404,11 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(FusedParams P) {
       for (int j = 0; j < kTokens; ++j) {
         const int t = min(ts + tile * kTokens + j, last);
         const bool is_new = fuse_new && t == pos;
-        const uint16_t *kp = is_new ? P.k_new + new_off : kbase + int64_t(t) * tok_stride;
-        const uint16_t *vp = is_new ? P.v_new + new_off : vbase + int64_t(t) * tok_stride;
+        const bool shared = t < P.shared;
+        const uint16_t *kp =
+            is_new ? P.k_new + new_off : (shared ? kbase0 : kbase) + int64_t(t) * tok_stride;
+        const uint16_t *vp =
+            is_new ? P.v_new + new_off : (shared ? vbase0 : vbase) + int64_t(t) * tok_stride;
         if constexpr (NT) {
           Tl.k[j] = load_stream(kp);
           Tl.v[j] = load_stream(vp);
@@ -725,6 +736,7 @@ int launch_decode_fused(const AttnArgs &a) {
   P.seqlens = a.seqlens;
   P.adv_seqlens = a.advance_seqlens;
   P.advance = a.advance_seqlens ? a.advance : 0;
+  P.shared = int(std::min<int64_t>(std::max<int64_t>(a.shared_prefix, 0), a.t_max));
   P.out = static_cast<uint16_t *>(a.out);
   P.B = int(a.batch);
   P.H = int(a.n_head);

@@ -36,6 +36,10 @@ struct AttnArgs {
   // the other paths launch launch_advance after their kernels. advance 0: positions only read.
   int32_t *advance_seqlens = nullptr;
   int advance = 0;
+  // Keys at positions [0, shared_prefix) hold the same K/V in every row (rows replicated from one
+  // prompt): the bf16 / head_dim 128 decode reads them from row 0 for every row, so the rows'
+  // repeated reads of those lines hit the caches. The other paths read each row's own copy.
+  int64_t shared_prefix = 0;
 };
 int launch_decode(const AttnArgs &a);
 int launch_prefill(const AttnArgs &a);

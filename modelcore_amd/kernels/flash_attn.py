@@ -132,7 +132,7 @@ def _window(window_size):
 # Public API: same interface as the reference (modelcore/kernels/flash_attn.py:270-366).
 # -----------------------------------------------------------------------------------------------
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
-                            causal=False, window_size=(-1, -1), *, advance=0):
+                            causal=False, window_size=(-1, -1), *, advance=0, shared_prefix=0):
     """Attention with KV cache for inference (modelcore/kernels/flash_attn.py:306-366).
 
     Args:
@@ -150,6 +150,12 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
             head_dim 128 path does it in its last kernel, so the step saves that launch. The host
             side of a KVCache then moves with KVCache.note_device_advance. 0 (default): the
             reference behaviour, cache_seqlens only read.
+        shared_prefix: extension, no counterpart in the reference operator. The caller's
+            statement that every row's K/V at positions [0, shared_prefix) equal row 0's (rows
+            replicated from one prompt, KVCache.prefill; KVCache.shared_prefix tracks it) and that
+            the new tokens land at or past it. The single-token bf16 / head_dim 128 path then
+            reads those keys from row 0 for every row: the same values and results, with the
+            rows' repeated reads served by the caches. 0 (default): each row's own keys.
 
     Returns:
         (B, T_new, H, D) tensor in q's dtype.
@@ -175,6 +181,9 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
     code = _ext.dtype_code(dt)
     seqlens = _check_seqlens(cache_seqlens, B, q.device)
     advance = int(advance)
+    shared_prefix = int(shared_prefix)
+    if not 0 <= shared_prefix <= T_max:
+        raise ValueError(f"shared_prefix {shared_prefix} outside [0, {T_max}]")
     if advance and seqlens.data_ptr() != cache_seqlens.data_ptr():
         raise ValueError("advance needs cache_seqlens itself to be contiguous (it is updated in "
                          "place)")
@@ -194,8 +203,8 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
             int(bool(causal)), code)
     ws_args = (ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
                _ext.stream_handle(q.device))
-    if advance:
-        st = lib.mcamd_flash_attn_with_kvcache_advance(*args, advance, *ws_args)
+    if advance or shared_prefix:
+        st = lib.mcamd_flash_attn_with_kvcache_ex(*args, advance, shared_prefix, *ws_args)
     else:
         st = lib.mcamd_flash_attn_with_kvcache(*args, *ws_args)
     _ext.check(st, "flash_attn_with_kvcache")
@@ -242,4 +251,7 @@ def flash_attn_func(q, k, v, causal=False, window_size=(-1, -1), doc_args=None):
 flash_attn = SimpleNamespace(
     flash_attn_func=flash_attn_func,
     flash_attn_with_kvcache=flash_attn_with_kvcache,
+    # Keyword arguments of flash_attn_with_kvcache beyond the reference's (callers check this
+    # before passing them, so that an operator without them can stand in).
+    EXTENSIONS=frozenset({"advance", "shared_prefix"}),
 )

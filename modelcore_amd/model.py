@@ -366,10 +366,20 @@ class Attention(nn.Module):
             k_cache, v_cache = kv_cache.get_slot_cache(self.kv_slot)
             y = self.attention.flash_attn_with_kvcache(q, k_cache, v_cache, k=k, v=v,
                                                        cache_seqlens=kv_cache.cache_seqlens,
-                                                       causal=True, window_size=window_size)
+                                                       causal=True, window_size=window_size,
+                                                       **self._extensions(kv_cache))
         if "output_gate" in self.features:
             y = self.features["output_gate"](y, x)
         return self.c_proj(y.contiguous().view(B, T, -1))
+
+    def _extensions(self, kv_cache):
+        """Operator keywords beyond the reference's, for an operator that takes them: the
+        cache's shared prompt prefix (rows replicated by KVCache.prefill), so the decode reads
+        it from row 0 for every row (same values, served by the caches)."""
+        shared = getattr(kv_cache, "shared_prefix", 0)
+        if shared and "shared_prefix" in getattr(self.attention, "EXTENSIONS", ()):
+            return {"shared_prefix": shared}
+        return {}
 
     def _forward_fused(self, x, q, k, v, kv_cache, kv_bus, qkv_part=None):
         """The same layer with the pre-attention ops fused: a producer rotates, norms and scales
@@ -394,7 +404,8 @@ class Attention(nn.Module):
             q = self.epilogue(q, self.rope.cos, self.rope.sin, seqlens, eps=self.norm.eps,
                               scale=1.2)
         y = self.attention.flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=seqlens,
-                                                   causal=True, window_size=(self.window, 0))
+                                                   causal=True, window_size=(self.window, 0),
+                                                   **self._extensions(kv_cache))
         if "output_gate" in self.features:
             y = self.features["output_gate"](y, x)
         return self.c_proj(y.contiguous().view(B, T, -1))

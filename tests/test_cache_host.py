@@ -30,6 +30,16 @@ def test_layout_and_initial_state_match_the_reference():
     assert k.shape == (3, T_MAX, H, D) and k.data_ptr() == c.k_cache[1].data_ptr()
 
 
+def test_shared_prefix_starts_at_zero_and_reset_clears_it():
+    c = _cache(3)
+    assert c.shared_prefix == 0
+    c.shared_prefix = 7
+    c.advance(9)
+    assert c.shared_prefix == 7
+    c.reset()
+    assert c.shared_prefix == 0
+
+
 def test_uniform_cache_reports_its_single_position():
     c = _cache(3)
     assert c.get_pos() == c.uniform_pos() == 0

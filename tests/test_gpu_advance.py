@@ -1,5 +1,5 @@
 """The operator with the decode step's position advance folded in
-(mcamd_flash_attn_with_kvcache_advance, flash_attn_with_kvcache(..., advance=n)).
+(mcamd_flash_attn_with_kvcache_ex, flash_attn_with_kvcache(..., advance=n)).
 
 Its outputs and cache contents must be bit-identical to the plain operator call followed by the
 separate advance (cache_seqlens += n, modelcore/cache.py:62-73), and every row's position must
@@ -71,10 +71,10 @@ def test_a_call_without_new_tokens_only_advances(dtype):
     c = make_case(seqlens, 1, 4, 2, 64, 16, dtype, seed=22)
     g = {n: t.to(DEV) for n, t in c.items()}
     lib = _ext.lib()
-    _ext.check(lib.mcamd_flash_attn_with_kvcache_advance(
+    _ext.check(lib.mcamd_flash_attn_with_kvcache_ex(
         g["q"].data_ptr(), None, None, g["k_cache"].data_ptr(), g["v_cache"].data_ptr(),
         g["cache_seqlens"].data_ptr(), g["q"].data_ptr(), 3, 0, 4, 2, 64, 16,
-        g["k_cache"].stride(0), -1, 1, _ext.dtype_code(dtype), 5, None, 0,
+        g["k_cache"].stride(0), -1, 1, _ext.dtype_code(dtype), 5, 0, None, 0,
         _ext.stream_handle(DEV)), "advance only")
     torch.cuda.synchronize()
     assert g["cache_seqlens"].tolist() == [9, 14, 5]

@@ -195,6 +195,38 @@ def test_sampling_decoder_rows_are_replicas_and_draws_are_reproducible():
     assert len({tuple(r.tolist()) for r in a}) > 1  # different seeds diverge
 
 
+def test_sampling_decoder_with_the_shared_prefix_read_matches_its_own_rows():
+    """The same flow decoded twice, once with the attention reading the replicated prompt's K/V
+    from row 0 for every row (KVCache.shared_prefix, set by prefill) and once with each row
+    reading its own copy: identical logits at every step and identical tokens."""
+    from modelcore_amd.sampling import PhiloxSampler
+    _note("sampling decoder, shared prefix")
+    cfg = mixed_window_config(n_layer=4)
+    mgr = gpu_manager(torch.bfloat16)
+    model = mgr.create_model(cfg, device=DEV, seed=0)
+    awake(model)
+    model.cache_inference_weights()
+    prompt = torch.randint(0, cfg.vocab_size, (150,), generator=torch.Generator().manual_seed(3))
+
+    def run(shared):
+        dec = mgr.new_decoder(model, prompt.tolist(), num_samples=8, max_tokens=10)
+        assert dec.kv_cache.shared_prefix == 150
+        if not shared:
+            dec.kv_cache.shared_prefix = 0
+        sampler = PhiloxSampler(8, DEV, base_seed=7)
+        toks, logits = [], []
+        for _ in range(10):
+            logits.append(dec.logits.clone())
+            t = sampler(dec.logits, 1.0).view(-1)
+            toks.append(t.cpu())
+            dec.step(t)
+        return torch.stack(toks, dim=1), torch.stack(logits)
+
+    (ta, la), (tb, lb) = run(True), run(False)
+    assert torch.equal(ta, tb)
+    assert torch.equal(la, lb)
+
+
 def test_cached_inference_weights_give_identical_logits():
     """The bf16 weight copies give the logits of the per-call casts bit for bit; stacking the
     QKV and gate/up copies into one product each changes only the GEMM's summation order."""
