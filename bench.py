@@ -695,8 +695,9 @@ def bench_sample(args):
     2048-token prompt (uniform random tokens, seed 0) at batch 1, replicates its cache into 64
     rows (KVCache.prefill), then decodes 512 tokens per row, each drawn on the device at
     temperature 1.0 from a per-row Philox stream (row r seeded r). The first --warmup steps are
-    untimed; the value is rows x timed steps / time. The decode attention reads the replicated
-    prompt's K/V from row 0 for every row (KVCache.shared_prefix) unless --no-shared-prefix."""
+    untimed; the value is rows x timed steps / time. The decode attention takes the replicated
+    prompt's K/V from row 0 for all rows (KVCache.shared_prefix: that part of the attention runs
+    on the matrix cores) unless --no-shared-prefix."""
     import torch
     from modelcore_amd import stats
     from modelcore_amd.model import ModelManager
@@ -755,7 +756,13 @@ def bench_sample(args):
                         if getattr(m, "_gate_up_blocked", False))
     kv = sum(stats.decode_step_bytes([SM_PROMPT + W + i] * SM_ROWS, SM_H, SM_HKV, D, 2)
              for i in range(K)) / K * SM_LAYERS
-    step_bytes = weight_bytes + kv
+    shared = dec.kv_cache.shared_prefix
+    # Bytes a step must read at least: with the prompt shared, its K/V once per layer and each
+    # row's own keys past it; otherwise every row's K/V (the reference's byte model).
+    kv_hbm = kv if not shared else (sum(
+        stats.decode_step_bytes([SM_PROMPT + W + i - shared] * SM_ROWS, SM_H, SM_HKV, D, 2)
+        for i in range(K)) / K + 2 * shared * SM_HKV * D * 2) * SM_LAYERS
+    step_bytes = weight_bytes + kv_hbm
     gbps = step_bytes / (ms * 1e-3) / 1e9
     hbm_peak, _, peak_src = peaks()
     result = {
@@ -780,11 +787,13 @@ def bench_sample(args):
                      "peak": hbm_peak / 1e9, "peak_source": peak_src, "unit": "GB/s",
                      "frac": round(gbps * 1e9 / hbm_peak, 4), "traffic": None,
                      "bytes_per_step": int(step_bytes), "weight_bytes": int(weight_bytes),
-                     "kv_bytes_per_step": int(kv),
-                     "kv_note": "every row's K/V counted, as the reference's byte model does; "
-                                "with shared_prefix > 0 the rows read the prompt's K/V from row "
-                                "0, so most of those reads are served by L2 and the memory-side "
-                                "cache rather than HBM"},
+                     "kv_bytes_per_step": int(kv_hbm),
+                     "kv_note": "with shared_prefix > 0 the prompt's K/V count once per layer "
+                                "(taken from row 0 for all rows, that part of the attention on "
+                                "the matrix cores) plus each row's own keys; the reference's byte "
+                                "model counts every row's K/V: reference_model_bytes_per_step",
+                     "reference_model_bytes_per_step": int(weight_bytes + kv),
+                     "reference_model_gbps": round((weight_bytes + kv) / (ms * 1e-3) / 1e9, 1)},
     }
     if not args.no_cpu_baseline:
         log("CPU baseline: one decode step of a 1-layer copy of the model on host cores")

@@ -78,8 +78,9 @@ int mcamd_kv_replicate(const void *src_k, const void *src_v, void *dst_k, void *
                        void *stream);
 
 /*
- * Bytes of scratch the attention entry points need for these sizes (split-K partials).
- * The caller allocates it (any 256-byte aligned device buffer) and passes it in.
+ * Bytes of scratch the attention entry points need for these sizes (split-K partials, and the
+ * matrix-core partials of a shared prefix where mcamd_flash_attn_with_kvcache_ex could take
+ * one). The caller allocates it (any 256-byte aligned device buffer) and passes it in.
  */
 size_t mcamd_attn_workspace_bytes(int64_t batch, int64_t t_new, int64_t n_head,
                                   int64_t n_kv_head, int64_t head_dim, int64_t t_max,
@@ -112,12 +113,19 @@ int mcamd_flash_attn_with_kvcache(const void *q, const void *k, const void *v,
  *  - shared_prefix (0 <= shared_prefix <= t_max): the caller states that every row's K and V at
  *    positions [0, shared_prefix) are the same as row 0's (rows replicated from one prompt), and
  *    that every new token lands at or past shared_prefix. For t_new == 1 with bf16 and head_dim
- *    128 those keys are then read from row 0 for every row -- the same values, so the same
- *    results -- and the rows' repeated reads of one row's lines are served by the caches instead
- *    of HBM. Other paths read each row's own copy. A statement that does not hold gives rows
- *    row 0's keys below shared_prefix.
- * With both 0 this is exactly mcamd_flash_attn_with_kvcache; otherwise outputs and cache contents
- * are bit-identical to that call (followed by the separate advance) whenever the statement holds.
+ *    128, those keys are then taken from row 0 for every row. With no window, a prefix of at
+ *    least 512 keys and at least 64 (row, query head) pairs per KV head, on the matrix cores:
+ *    all rows' queries against row 0's prefix in key ranges, merged with the decode pass over
+ *    each row's own keys -- the sums run in another order, so outputs agree with the call
+ *    without it within bf16 rounding, not bit for bit (this needs the workspace size of
+ *    mcamd_attn_workspace_bytes(); a smaller one that still covers the decode pass takes the
+ *    other way). Otherwise the decode pass reads them from row 0 itself: the same values in the
+ *    same order, so the same results bit for bit, with the rows' repeated reads of one row's
+ *    lines served by the caches. Other paths read each row's own copy. A statement that does not
+ *    hold gives rows row 0's keys below shared_prefix.
+ * With both 0 this is exactly mcamd_flash_attn_with_kvcache; otherwise the cache contents are
+ * bit-identical to that call's (followed by the separate advance) whenever the statement holds,
+ * and the outputs as described above.
  * Replaces flash_attn_with_kvcache followed by KVCache.advance(advance) in a decode step
  * (modelcore/kernels/flash_attn.py:306-366, then modelcore/model.py:99-100 ->
  * modelcore/cache.py:62-73), after KVCache.prefill's replication (modelcore/cache.py:75-90).

@@ -64,7 +64,10 @@ extern "C" size_t mcamd_attn_workspace_bytes(int64_t batch, int64_t t_new, int64
                                              int64_t n_kv_head, int64_t head_dim, int64_t t_max,
                                              int64_t window) {
   if (t_new != 1 || batch <= 0 || n_kv_head <= 0 || n_head < n_kv_head) return 0;
-  return decode_workspace_bytes(batch, n_head, n_kv_head, head_dim, t_max, window);
+  // Room for the shared-prefix partials too, where the fused decode can take a shared prefix on
+  // the matrix cores; a workspace of decode_workspace_bytes() alone still serves every call.
+  return decode_workspace_bytes(batch, n_head, n_kv_head, head_dim, t_max, window) +
+         decode_prefix_bytes(batch, n_head, n_kv_head, head_dim, window);
 }
 
 extern "C" int mcamd_decode_attention(const void *q, const void *k_cache, const void *v_cache,

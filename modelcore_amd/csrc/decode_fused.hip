@@ -41,9 +41,15 @@
 //  * Append: the segment that ends at p reads the new token from k/v instead of the cache and
 //    its lanes store it into the cache at p (bit-exact copy; the first query-head group only).
 //  * Shared prefix: when the caller states that every row's keys [0, S) are copies of row 0's
-//    (rows replicated from one prompt), those keys are read from row 0 for every row. The values
-//    are the same, so are the results; the rows' repeated reads of one row's lines are served by
-//    L2 and the memory-side cache instead of HBM.
+//    (rows replicated from one prompt), those keys come from row 0 for every row. A wide batch
+//    with no window (at least 64 (row, query head) pairs per KV head, S >= 512) takes them on the
+//    matrix cores first (the chunked-prefill kernel in its prefix mode: every row's queries
+//    against row 0's keys, in up to sixteen key ranges, as partial slots of each unit); this pass
+//    then covers each row's keys from S on and writes partials even for a single segment, and
+//    the merge folds the prefix partials in (sums in another order: within bf16 rounding of the
+//    unshared call). Otherwise this pass reads the keys below S from row 0 itself: the same
+//    values in the same order, the same results, with the rows' repeated reads of one row's
+//    lines served by L2 and the memory-side cache instead of HBM.
 #include "kernels.h"
 
 #include <cmath>
@@ -52,8 +58,8 @@ namespace mcamd {
 namespace {
 
 constexpr int D = 128;
-constexpr int GM = 4;                 // query heads per KV head in one unit
-constexpr int KG = 4;                 // KV heads per unit (one per row of 16 lanes)
+constexpr int GM = kDecodeUnitQ;      // query heads per KV head in one unit
+constexpr int KG = kDecodeUnitKv;     // KV heads per unit (one per row of 16 lanes)
 constexpr int kTokens = 4;            // tokens per tile
 constexpr float kRescaleSlack = 8.f;  // log2 units
 constexpr int kMaxGroups = 1024;      // 4-wave workgroups per launch, at most
@@ -80,7 +86,8 @@ constexpr int kMergeDims = 128 / 16 / kMergeSplit;  // dims per lane in that mer
 #define MCAMD_DECODE_SEG_COST 64
 #endif
 constexpr int kSegCost = MCAMD_DECODE_SEG_COST;  // key-free lead slots per unit (see unit_span)
-constexpr int kPart = KG * GM * D + 2 * KG * GM;  // floats per partial: o[16][D], (m, l)[16]
+constexpr int kPart = kDecodePartFloats;  // floats per partial: o[16][D], (m, l)[16]
+static_assert(kPart == KG * GM * D + 2 * KG * GM, "partial slot layout");
 #ifndef MCAMD_DECODE_BUCKET
 #define MCAMD_DECODE_BUCKET 16
 #endif
@@ -95,6 +102,11 @@ constexpr int kBucket = MCAMD_DECODE_BUCKET;
 // when its units average fewer segments (see launch_decode_fused).
 constexpr int kSpec = MCAMD_DECODE_SPEC;
 constexpr int64_t kTemporalLimit = int64_t(64) << 20;  // bytes of K/V: see launch_decode_fused
+constexpr int64_t kPrefixMinKeys = 512;       // shorter shared prefixes stay in this pass
+#ifndef MCAMD_PREFIX_KEYS
+#define MCAMD_PREFIX_KEYS 128
+#endif
+constexpr int64_t kPrefixKeysPerSplit = MCAMD_PREFIX_KEYS;  // keys per matrix-core workgroup, at least
 static_assert(kSpec <= kBucket, "speculative merge loads stay inside the unit's bucket");
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -111,6 +123,11 @@ struct FusedParams {
   int32_t *adv_seqlens;  // the merge pass adds `advance` to every row's position (0: it does not)
   int advance;
   int shared;  // keys [0, shared) are read from row 0 for every row
+  // Prefix on the matrix cores: this pass covers keys from lo_floor on, and the merge pass also
+  // folds in n_pre partials per unit (slots unit * n_pre + j of `pre`) made for keys below it.
+  int lo_floor;
+  const float *pre;
+  int n_pre;
   int B, H, H_kv, G, n_hc, n_kg, n_units, T_max, window, n_groups;
   int scan32;  // B <= 64 and every sum of row slot counts fits in 31 bits
   int64_t cache_b;
@@ -189,8 +206,8 @@ __device__ __forceinline__ int row_keys(const FusedParams &P, int b, int &lo) {
     lo = 0;
     return 0;
   }
-  lo = key_lo(pos, P.window);
-  return pos - lo + 1;
+  lo = max(key_lo(pos, P.window), P.lo_floor);
+  return max(pos - lo + 1, 0);
 }
 
 // Slots a unit of a row with nk keys takes in the work split: kSegCost lead slots that hold no
@@ -595,7 +612,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(FusedParams P) {
     // The workgroup holding the unit's first key tells the merge pass where the unit's
     // partials are, so that it need not rebuild the work split from cache_seqlens.
     if (g == g_first && threadIdx.x == 0) P.desc[ug] = make_int2(g_first, g_last - g_first + 1);
-    if (g_first == g_last) {
+    if (g_first == g_last && P.n_pre == 0) {
       if (m_live) write_out(acc, L);  // the segment is the whole unit
     } else {
       // This workgroup's partial for the unit, segment j = g - g_first: bucket slot j of the
@@ -633,7 +650,9 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(FusedParams P) {
 // follow BATCH at a time. The pass does not read cache_seqlens (the descriptors carry all it
 // needs), so it can also advance the positions: the wave of each row's first unit and head adds
 // `advance` to the row's entry.
-template <int SPEC>
+// PRE: also fold in the unit's n_pre partials of the shared prefix (loaded with the rest, in
+// the same round trip); a unit's single segment is then a partial too.
+template <int SPEC, bool PRE>
 __global__ __launch_bounds__(64) void decode_merge_kernel(FusedParams P) {
   constexpr int BATCH = 8;
   const int lane = threadIdx.x;
@@ -661,8 +680,19 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(FusedParams P) {
     ml[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * hr);
     v[k] = *reinterpret_cast<const float2 *>(ps + hr * D + 2 * lane);
   }
+  constexpr int NP = PRE ? kPrefixMaxSplits : 1;
+  float2 pml[NP], pv[NP];
+  if constexpr (PRE) {
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      const float *ps = P.pre + (int64_t(ug) * P.n_pre + min(k, P.n_pre - 1)) * kPart;
+      pml[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * hr);
+      pv[k] = *reinterpret_cast<const float2 *>(ps + hr * D + 2 * lane);
+    }
+  }
   const int g_first = d.x, nseg = d.y;
-  if (nseg <= 1) return;  // no keys, or written directly by the streaming pass
+  // No keys (a row outside the cache: NaN written), or a unit written directly.
+  if (nseg == 0 || (!PRE && nseg == 1)) return;
   float M = -INFINITY, L = 0.f, t0 = 0.f, t1 = 0.f;
   auto add = [&](float2 mlk, float2 vk, bool valid) {
     const float mk = valid ? mlk.x : -INFINITY;
@@ -685,6 +715,10 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(FusedParams P) {
     }
 #pragma unroll
     for (int k = 0; k < BATCH; ++k) add(mb[k], vb[k], s0 + k < nseg);
+  }
+  if constexpr (PRE) {
+#pragma unroll
+    for (int k = 0; k < NP; ++k) add(pml[k], pv[k], k < P.n_pre);
   }
   const float inv = 1.f / L;
   *reinterpret_cast<uint32_t *>(P.out + (int64_t(b) * P.H + int64_t(kvh) * P.G + hc * GM + hh) * D +
@@ -718,6 +752,16 @@ size_t decode_fused_partial_bytes(int64_t batch, int64_t n_head, int64_t n_kv_he
   (void)window;
   const int64_t units = batch * decode_fused_units(n_head, n_kv_head);
   return size_t((units * kBucket + kMaxGroups + units) * kPart * 4 + units * int64_t(sizeof(int2)));
+}
+
+size_t decode_prefix_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
+                           int64_t window) {
+  // Worth it for many queries per KV head (rows x query heads fill most of the matrix-core
+  // kernel's 256 pairs) and without a window (its keys would then differ per row).
+  if (head_dim != D || window >= 0 || n_kv_head <= 0 || batch * (n_head / n_kv_head) < 64)
+    return 0;
+  const int64_t units = batch * decode_fused_units(n_head, n_kv_head);
+  return size_t(units * kPrefixMaxSplits * kPart * 4);
 }
 
 bool decode_fused_supported(const AttnArgs &a) {
@@ -763,6 +807,26 @@ int launch_decode_fused(const AttnArgs &a) {
   P.part = reinterpret_cast<float *>(ws);
   P.over = P.part + units * kBucket * kPart;
   P.desc = reinterpret_cast<int2 *>(P.over + (kMaxGroups + units) * kPart);
+  // A long shared prompt prefix of a wide batch goes to the matrix cores (every row's queries
+  // against row 0's prefix keys at once, in key ranges) when the workspace has room for those
+  // partials; this pass then covers each row's own keys only, and the merge folds both.
+  P.lo_floor = 0;
+  P.pre = nullptr;
+  P.n_pre = 0;
+  const size_t base_ws =
+      decode_workspace_bytes(a.batch, a.n_head, a.n_kv_head, a.head_dim, a.t_max, a.window);
+  const size_t pre_ws = decode_prefix_bytes(a.batch, a.n_head, a.n_kv_head, a.head_dim, a.window);
+  if (pre_ws > 0 && a.shared_prefix >= kPrefixMinKeys && a.workspace_bytes >= base_ws + pre_ws) {
+    P.n_pre = int(std::min<int64_t>(kPrefixMaxSplits, a.shared_prefix / kPrefixKeysPerSplit));
+    P.lo_floor = int(a.shared_prefix);
+    float *pre = reinterpret_cast<float *>(ws + base_ws);
+    P.pre = pre;
+    PrefixArgs pa{a.q,     a.k_cache,   a.v_cache, pre,
+                  a.batch, a.n_head,    a.n_kv_head, a.t_max,
+                  a.cache_batch_stride, a.shared_prefix, P.n_pre, a.stream};
+    const int st = launch_prefix_partials(pa);
+    if (st != MCAMD_OK) return st;
+  }
   // K/V bytes the call can read (every row at its longest span). A call that fits in a quarter
   // of the 256 MB memory-side cache loads them with the default policy, so a KV-sharing layer
   // that reads the same slot next finds them there (measured on the 24-layer mixed-window stack:
@@ -783,12 +847,19 @@ int launch_decode_fused(const AttnArgs &a) {
   // 32-layer sampling decode: 6.71 -> 6.62 ms per step with 4 slots; 16 kept where units span
   // many workgroups, as in the 32-row microbench and the mixed-window stack).
   const int64_t per_unit = groups / std::max<int64_t>(1, units) + 2;
-  if (kSpec >= 16 && per_unit > 8)
-    hipLaunchKernelGGL(decode_merge_kernel<(kSpec < 16 ? kSpec : 16)>, merge_grid, dim3(64), 0, a.stream, P);
+  auto merge = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, merge_grid, dim3(64), 0, a.stream, P);
+  };
+  constexpr int S16 = kSpec < 16 ? kSpec : 16, S8 = kSpec < 8 ? kSpec : 8,
+                S4 = kSpec < 4 ? kSpec : 4;
+  if (P.n_pre > 0)
+    merge(decode_merge_kernel<S4, true>);
+  else if (kSpec >= 16 && per_unit > 8)
+    merge(decode_merge_kernel<S16, false>);
   else if (per_unit > 4)
-    hipLaunchKernelGGL(decode_merge_kernel<(kSpec < 8 ? kSpec : 8)>, merge_grid, dim3(64), 0, a.stream, P);
+    merge(decode_merge_kernel<S8, false>);
   else
-    hipLaunchKernelGGL(decode_merge_kernel<(kSpec < 4 ? kSpec : 4)>, merge_grid, dim3(64), 0, a.stream, P);
+    merge(decode_merge_kernel<S4, false>);
   return launch_status("decode_merge");
 }
 

@@ -53,6 +53,34 @@ int64_t decode_max_splits(int64_t t_max, int64_t window);
 size_t decode_workspace_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
                               int64_t t_max, int64_t window);
 
+// Units of the fused decode: one row's group of kDecodeUnitKv KV heads and kDecodeUnitQ query
+// heads of each. A partial slot holds o[kv][q][128] then (m, l)[kv][q], fp32.
+constexpr int kDecodeUnitKv = 4;
+constexpr int kDecodeUnitQ = 4;
+constexpr int kDecodePartFloats =
+    kDecodeUnitKv * kDecodeUnitQ * 128 + 2 * kDecodeUnitKv * kDecodeUnitQ;
+
+// Shared prompt prefix on the matrix cores: for every KV head, the queries of all rows against
+// keys [0, prefix) of row 0, in n_split key ranges; each range's unnormalised (o, m, l) per
+// (row, query head) goes to the fused decode's partial-slot layout, slot (unit * n_split +
+// range), for its merge pass to fold in.
+#ifndef MCAMD_PREFIX_SPLITS
+#define MCAMD_PREFIX_SPLITS 16
+#endif
+constexpr int kPrefixMaxSplits = MCAMD_PREFIX_SPLITS;
+struct PrefixArgs {
+  const void *q, *k_cache, *v_cache;
+  float *part;
+  int64_t rows, n_head, n_kv_head, t_max, cache_batch_stride, prefix;
+  int n_split;
+  hipStream_t stream;
+};
+int launch_prefix_partials(const PrefixArgs &a);
+// Bytes of workspace past decode_workspace_bytes() for those partials (0 where the fused decode
+// never takes the prefix on the matrix cores).
+size_t decode_prefix_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
+                           int64_t window);
+
 // The fused bf16 / head_dim 128 decode (append + split-K + merge in one launch).
 bool decode_fused_supported(const AttnArgs &a);
 int launch_decode_fused(const AttnArgs &a);

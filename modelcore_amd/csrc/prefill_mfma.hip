@@ -45,6 +45,10 @@
 // 16-byte reads against ~100 B/clk contiguous; 134 B/clk for the swizzled transpose reads).
 // In the matrix phase the LDS reads of the next 16-key step are issued (as inline asm, with
 // explicit waits) before the products of the current one, so the LDS streams under the MFMAs.
+//
+// Prefix mode (launch_prefix_partials): the same kernel serves a decode step whose rows share a
+// replicated prompt prefix -- the "positions" are the decode rows, the keys a range of row 0's
+// prefix, and the unnormalised (o, m, l) go to the fused decode's partial slots.
 #include "kernels.h"
 
 #include <cmath>
@@ -74,6 +78,9 @@ struct MfmaParams {
   int T_new, H, H_kv, G, QT, T_max, window, n_bh;
   int64_t cache_b;
   float scale_log2;
+  // Prefix mode only: the partial slots, the key ranges and the fused decode's unit geometry.
+  float *part;
+  int n_split, key_len, prefix, n_qt, n_units, n_hc;
 };
 
 __device__ __forceinline__ f32x16 mfma(const bf16x8 &a, const bf16x8 &b, const f32x16 &c) {
@@ -123,12 +130,19 @@ __device__ __forceinline__ float exp2_or_zero(float x) {
   return x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(x);
 }
 
+// PREFIX = false: the chunked prefill. PREFIX = true: the shared prompt prefix of a decode step
+// -- the "positions" of a workgroup are decode rows (q is (rows, 1, H, D), the same layout as
+// (1, rows, H, D)), every query attends keys [lo, hi] of row 0 (key range `split` of the
+// prefix, all of them before every row's position, so no causal mask: the pairs are placed at
+// position hi), and the unnormalised (o, m, l) go to the fused decode's partial slots.
+template <bool PREFIX>
 __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P) {
   __shared__ __attribute__((aligned(1024))) uint16_t sK[4][TILE];
   __shared__ __attribute__((aligned(1024))) uint16_t sV[4][TILE];
 
   const int bh = blockIdx.x % P.n_bh;
-  const int qt = blockIdx.x / P.n_bh;
+  const int qt = PREFIX ? (blockIdx.x / P.n_bh) % P.n_qt : blockIdx.x / P.n_bh;
+  const int split = PREFIX ? blockIdx.x / (P.n_bh * P.n_qt) : 0;
   const int b = bh / P.H_kv;
   const int kvh = bh - b * P.H_kv;
   const int q0 = qt * P.QT;
@@ -138,15 +152,16 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
   const int h = lane >> 5;    // lane half
   const int col = lane & 31;  // this lane's pair within the wave's 32
 
-  const int s0 = P.seqlens[b];
+  const int s0 = PREFIX ? 0 : P.seqlens[b];
   const int q_end = min(q0 + P.QT, P.T_new);  // positions [q0, q_end) of the chunk
-  const bool row_ok = s0 >= 0 && int64_t(s0) + P.T_new <= P.T_max;
+  const bool row_ok = PREFIX || (s0 >= 0 && int64_t(s0) + P.T_new <= P.T_max);
 
   const int pr = wave * 32 + col;
   const bool live = pr < P.QT * P.G && q0 + pr / P.G < q_end;
   const int pos = live ? q0 + pr / P.G : q0;  // dead pairs compute on a live position
   const int head = live ? pr - (pr / P.G) * P.G : 0;
-  uint16_t *out = P.out + ((int64_t(b) * P.T_new + pos) * P.H + int64_t(kvh) * P.G + head) * D;
+  uint16_t *out =
+      PREFIX ? nullptr : P.out + ((int64_t(b) * P.T_new + pos) * P.H + int64_t(kvh) * P.G + head) * D;
   if (!row_ok) {
     if (live)
       for (int d = h * 64; d < h * 64 + 64; ++d) out[d] = 0x7fc0;
@@ -162,10 +177,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
     for (int kd = 0; kd < 8; ++kd)
       qf[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(qp + 16 * kd));
   }
-  const int p_abs = s0 + pos;
-  const int p_first = s0 + q0;
-  const int p_last = s0 + q_end - 1;
-  const int lo = P.window >= 0 ? max(0, p_first - P.window) : 0;
+  // Prefix mode: key range [split * key_len, min(prefix, (split + 1) * key_len)), every pair at
+  // its last key (so the causal rule masks exactly the keys past the range).
+  const int r_hi = PREFIX ? min(P.prefix, (split + 1) * P.key_len) - 1 : 0;
+  const int p_abs = PREFIX ? r_hi : s0 + pos;
+  const int p_first = PREFIX ? r_hi : s0 + q0;
+  const int p_last = PREFIX ? r_hi : s0 + q_end - 1;
+  const int lo = PREFIX ? split * P.key_len : P.window >= 0 ? max(0, p_first - P.window) : 0;
   const int hi = p_last;
 
   const int64_t tok = int64_t(P.H_kv) * D;
@@ -431,6 +449,27 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
 
   // Normalise and write: o[md][4j + i] is dim 32 md + 8 j + 4 h + i of pair `col`.
   const float lt = sum_halves(l);
+  if constexpr (PREFIX) {
+    // The unnormalised partial of (row pos, head) for this key range, in the decode unit's slot:
+    // unit (pos, KV-head group, query-head group), entry (KV head, query head) within it.
+    if (!live) return;
+    const int g_head = head;
+    const int unit = (kvh / kDecodeUnitKv) * P.n_hc + g_head / kDecodeUnitQ;
+    const int entry = (kvh % kDecodeUnitKv) * kDecodeUnitQ + g_head % kDecodeUnitQ;
+    float *slot =
+        P.part + ((int64_t(pos) * P.n_units + unit) * P.n_split + split) * kDecodePartFloats;
+    float *po = slot + entry * D;
+#pragma unroll
+    for (int md = 0; md < 4; ++md)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<float4 *>(po + 32 * md + 8 * j + 4 * h) =
+            make_float4(o[md][4 * j], o[md][4 * j + 1], o[md][4 * j + 2], o[md][4 * j + 3]);
+    if (h == 0)
+      *reinterpret_cast<float2 *>(slot + kDecodeUnitKv * kDecodeUnitQ * D + 2 * entry) =
+          make_float2(m, lt);
+    return;
+  }
   const float inv = 1.f / lt;
   if (!live) return;
 #pragma unroll
@@ -478,8 +517,39 @@ int launch_prefill_mfma(const AttnArgs &a) {
   const int64_t n_qt = (a.t_new + P.QT - 1) / P.QT;
   const int64_t blocks = n_qt * P.n_bh;
   if (blocks > 0x7fffffff) return fail(MCAMD_EUNSUPPORTED, "prefill: grid too large");
-  hipLaunchKernelGGL(prefill_mfma_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0, a.stream, P);
+  hipLaunchKernelGGL(prefill_mfma_kernel<false>, dim3(unsigned(blocks)), dim3(kThreads), 0,
+                     a.stream, P);
   return launch_status("prefill_mfma");
+}
+
+int launch_prefix_partials(const PrefixArgs &a) {
+  MfmaParams P{};
+  P.q = static_cast<const uint16_t *>(a.q);
+  P.k_cache = static_cast<const uint16_t *>(a.k_cache);
+  P.v_cache = static_cast<const uint16_t *>(a.v_cache);
+  P.seqlens = nullptr;
+  P.out = nullptr;
+  P.T_new = int(a.rows);
+  P.H = int(a.n_head);
+  P.H_kv = int(a.n_kv_head);
+  P.G = int(a.n_head / a.n_kv_head);
+  P.QT = kPairs / P.G;
+  P.T_max = int(a.t_max);
+  P.window = -1;
+  P.n_bh = int(a.n_kv_head);  // row 0 only
+  P.cache_b = a.cache_batch_stride;
+  P.scale_log2 = float(kLog2e / std::sqrt(double(D)));
+  P.part = a.part;
+  P.n_split = a.n_split;
+  P.key_len = int((a.prefix + a.n_split - 1) / a.n_split);
+  P.prefix = int(a.prefix);
+  P.n_qt = int((a.rows + P.QT - 1) / P.QT);
+  P.n_hc = (P.G + kDecodeUnitQ - 1) / kDecodeUnitQ;
+  P.n_units = ((P.H_kv + kDecodeUnitKv - 1) / kDecodeUnitKv) * P.n_hc;
+  const int64_t blocks = int64_t(P.n_qt) * P.n_bh * P.n_split;
+  hipLaunchKernelGGL(prefill_mfma_kernel<true>, dim3(unsigned(blocks)), dim3(kThreads), 0,
+                     a.stream, P);
+  return launch_status("prefill_mfma prefix");
 }
 
 }  // namespace mcamd

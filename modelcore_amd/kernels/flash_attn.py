@@ -154,8 +154,11 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
             statement that every row's K/V at positions [0, shared_prefix) equal row 0's (rows
             replicated from one prompt, KVCache.prefill; KVCache.shared_prefix tracks it) and that
             the new tokens land at or past it. The single-token bf16 / head_dim 128 path then
-            reads those keys from row 0 for every row: the same values and results, with the
-            rows' repeated reads served by the caches. 0 (default): each row's own keys.
+            takes those keys from row 0: on the matrix cores for all rows at once when there is
+            no window, the prefix has >= 512 keys and rows x query heads per KV head >= 64
+            (outputs within bf16 rounding of the call without it: the sums run in another
+            order), else read by the decode pass from row 0 (bit-identical outputs, the rows'
+            repeated reads served by the caches). 0 (default): each row's own keys.
 
     Returns:
         (B, T_new, H, D) tensor in q's dtype.

@@ -60,8 +60,17 @@ def test_workspace_size_follows_the_split_count():
     # area of 1024 + units slots, then one (first group, segments) int pair per unit
     # (H = 16 query heads over 4 KV heads: one unit per row)
     fused = (16 * B + 1024 + B) * (16 * (D + 2)) * 4 + B * 8
+    # and, with no window and rows x query heads >= 64, sixteen shared-prefix partial slots per
+    # unit past that (32 rows x 4 query heads per KV head here)
+    prefix = B * 16 * (16 * (D + 2)) * 4
+    base = -(-max(general, fused) // 256) * 256
     got = lib.mcamd_attn_workspace_bytes(B, 1, H, 4, D, T_max, -1)
-    assert max(general, fused) <= got < max(general, fused) + 256  # scratch only, no counters
+    assert got == base + prefix  # scratch only, no counters
+    # 8 rows x 4 query heads per KV head: too few for the matrix cores, no prefix slots
+    general8 = 8 * H * n_splits * (D + 2) * 4
+    fused8 = (16 * 8 + 1024 + 8) * (16 * (D + 2)) * 4 + 8 * 8
+    assert lib.mcamd_attn_workspace_bytes(8, 1, H, 4, D, T_max, -1) == \
+        -(-max(general8, fused8) // 256) * 256
     windowed = lib.mcamd_attn_workspace_bytes(B, 1, H, 4, D, T_max, 1024)
     assert windowed <= got
     fp32 = lib.mcamd_attn_workspace_bytes(B, 1, H, 4, 64, T_max, 1024)  # general kernel only

@@ -195,10 +195,12 @@ def test_sampling_decoder_rows_are_replicas_and_draws_are_reproducible():
     assert len({tuple(r.tolist()) for r in a}) > 1  # different seeds diverge
 
 
-def test_sampling_decoder_with_the_shared_prefix_read_matches_its_own_rows():
-    """The same flow decoded twice, once with the attention reading the replicated prompt's K/V
-    from row 0 for every row (KVCache.shared_prefix, set by prefill) and once with each row
-    reading its own copy: identical logits at every step and identical tokens."""
+def test_sampling_decoder_with_the_shared_prefix_matches_its_own_rows():
+    """The same flow decoded twice, teacher-forced on one token stream: once with the attention
+    taking the replicated prompt's K/V from row 0 (KVCache.shared_prefix, set by prefill; 32 rows
+    x 3 query heads per KV head put the prompt on the matrix cores) and once with each row reading
+    its own copy. The prefill logits are identical; the decode logits agree within the bf16
+    rounding of the reordered sums."""
     from modelcore_amd.sampling import PhiloxSampler
     _note("sampling decoder, shared prefix")
     cfg = mixed_window_config(n_layer=4)
@@ -206,25 +208,22 @@ def test_sampling_decoder_with_the_shared_prefix_read_matches_its_own_rows():
     model = mgr.create_model(cfg, device=DEV, seed=0)
     awake(model)
     model.cache_inference_weights()
-    prompt = torch.randint(0, cfg.vocab_size, (150,), generator=torch.Generator().manual_seed(3))
-
-    def run(shared):
-        dec = mgr.new_decoder(model, prompt.tolist(), num_samples=8, max_tokens=10)
-        assert dec.kv_cache.shared_prefix == 150
-        if not shared:
-            dec.kv_cache.shared_prefix = 0
-        sampler = PhiloxSampler(8, DEV, base_seed=7)
-        toks, logits = [], []
-        for _ in range(10):
-            logits.append(dec.logits.clone())
-            t = sampler(dec.logits, 1.0).view(-1)
-            toks.append(t.cpu())
-            dec.step(t)
-        return torch.stack(toks, dim=1), torch.stack(logits)
-
-    (ta, la), (tb, lb) = run(True), run(False)
-    assert torch.equal(ta, tb)
-    assert torch.equal(la, lb)
+    prompt = torch.randint(0, cfg.vocab_size, (600,), generator=torch.Generator().manual_seed(3))
+    rows, steps = 32, 8
+    shared = mgr.new_decoder(model, prompt.tolist(), num_samples=rows, max_tokens=steps)
+    own = mgr.new_decoder(model, prompt.tolist(), num_samples=rows, max_tokens=steps)
+    assert shared.kv_cache.shared_prefix == 600
+    own.kv_cache.shared_prefix = 0
+    assert torch.equal(shared.logits, own.logits)
+    sampler = PhiloxSampler(rows, DEV, base_seed=7)
+    for i in range(steps):
+        t = sampler(shared.logits, 1.0).view(-1)
+        shared.step(t)
+        own.step(t)
+        err = (shared.logits.float() - own.logits.float()).abs().max().item()
+        scale = own.logits.float().abs().max().item()
+        print(f"step {i}: logits max-abs {err:.5f} (scale {scale:.3f})", flush=True)
+        assert err <= 0.05, f"step {i}: logits max-abs {err}"
 
 
 def test_cached_inference_weights_give_identical_logits():

@@ -1,17 +1,23 @@
 """The decode operator's shared-prefix read (flash_attn_with_kvcache(..., shared_prefix=P),
 mcamd_flash_attn_with_kvcache_ex): when every row's K/V at positions [0, P) are copies of row
-0's -- rows replicated from one prompt by KVCache.prefill -- the bf16 / head_dim 128 decode reads
-those keys from row 0 for every row. The values are the same, so outputs and cache contents must
-be bit-identical to the call without it, on every path (the other paths read each row's own copy)
-and for windows that end inside and outside the prefix. A planted difference in row 1's prefix
-shows the reads really come from row 0, and a run of the sampling decoder gives the same tokens
-and logits with and without it.
+0's -- rows replicated from one prompt by KVCache.prefill -- the bf16 / head_dim 128 decode takes
+those keys from row 0 for every row, in one of two ways:
+  * few queries per KV head, a short prefix or a window: the decode pass reads them from row 0
+    itself; the values are the same, so outputs must be bit-identical to the call without it;
+  * rows x query heads >= 64, no window, P >= 512: the prefix goes to the matrix cores (all rows'
+    queries against row 0's prefix keys, in key ranges) and the decode pass covers each row's
+    own keys; the partial sums then run in another order, so outputs must match the float64
+    oracle within the bf16 tolerance and the call without it within a few bf16 units.
+The caches must be bit-identical either way (the append does not change). A planted difference
+in row 1's prefix shows the reads come from row 0, and the sampling decoder gives the same logits
+with and without it, teacher-forced on one token stream.
 """
 import numpy as np
 import pytest
 import torch
 
-from _util import bits, make_case
+from _util import ATOL, bits, make_case, max_abs, to_np
+from oracle import kv_oracle as ko
 from modelcore_amd.kernels.flash_attn import flash_attn
 
 pytestmark = pytest.mark.gpu
@@ -40,27 +46,61 @@ def _call(c, window, shared):
     return out, g
 
 
-CASES = [
-    # dtype, P, seqlens (all >= P), H, H_kv, D, T_max, window
+def _rows(n, lo, hi, seed):
+    return [int(x) for x in np.random.default_rng(seed).integers(lo, hi, n)]
+
+
+PREFIX_CASES = [
+    # dtype, P, seqlens (all >= P), H, H_kv, D, T_max: the prefix on the matrix cores (key
+    # ranges of at least 128 keys, at most sixteen)
+    (torch.bfloat16, 2048, [2048] + _rows(63, 2048, 2560, 1), 32, 8, 128, 2560),
+    (torch.bfloat16, 600, _rows(32, 600, 900, 2), 12, 4, 128, 1000),       # G = 3, 4 ranges
+    (torch.bfloat16, 1000, _rows(100, 1000, 1100, 3), 16, 4, 128, 1200),   # 400 pairs: 2 tiles
+    (torch.bfloat16, 777, _rows(40, 777, 800, 4), 64, 8, 128, 900),        # G = 8, 6 ranges
+]
+
+READ_CASES = [
+    # dtype, P, seqlens (all >= P), H, H_kv, D, T_max, window: the decode pass reads the prefix
+    # from row 0 itself (32 pairs per KV head, or a window), or the general path ignores it
     (torch.bfloat16, 2048, [2048, 2100, 2559, 2300, 2049, 2200, 2400, 2048], 32, 8, 128, 2600, -1),
     (torch.bfloat16, 700, [700, 705, 1200, 900], 16, 4, 128, 1300, -1),
     (torch.bfloat16, 700, [700, 705, 1200, 900], 16, 4, 128, 1300, 64),    # windows: inside, across
     (torch.bfloat16, 700, [700, 705, 1200, 900], 16, 4, 128, 1300, 300),   # and past the prefix
+    (torch.bfloat16, 2048, [2048] + _rows(63, 2048, 2560, 5), 32, 8, 128, 2560, 600),
     (torch.bfloat16, 64, [64, 80, 64], 8, 2, 64, 128, -1),                 # general path: ignored
     (torch.float32, 64, [64, 80, 64], 8, 2, 128, 128, -1),
 ]
 
 
-@pytest.mark.parametrize("dtype,P,seqlens,H,H_kv,D,T_max,window", CASES)
+@pytest.mark.parametrize("dtype,P,seqlens,H,H_kv,D,T_max,window", READ_CASES)
 def test_shared_prefix_reads_give_bit_identical_results(dtype, P, seqlens, H, H_kv, D, T_max,
                                                         window):
-    _note("shared prefix", dtype, P, seqlens, H, H_kv, D, T_max, window)
+    _note("shared prefix, read", dtype, P, len(seqlens), H, H_kv, D, T_max, window)
     c = _replicated(seqlens, P, H, H_kv, D, T_max, dtype, seed=41)
     want, gw = _call(c, window, 0)
     got, gg = _call(c, window, P)
     assert np.array_equal(bits(got), bits(want)), "outputs differ"
     assert np.array_equal(bits(gg["k_cache"]), bits(gw["k_cache"]))
     assert np.array_equal(bits(gg["v_cache"]), bits(gw["v_cache"]))
+
+
+@pytest.mark.parametrize("dtype,P,seqlens,H,H_kv,D,T_max", PREFIX_CASES)
+def test_shared_prefix_on_the_matrix_cores_matches_the_oracle(dtype, P, seqlens, H, H_kv, D,
+                                                              T_max):
+    _note("shared prefix, matrix cores", dtype, P, len(seqlens), H, H_kv, D, T_max)
+    c = _replicated(seqlens, P, H, H_kv, D, T_max, dtype, seed=44)
+    want, gw = _call(c, -1, 0)
+    got, gg = _call(c, -1, P)
+    assert np.array_equal(bits(gg["k_cache"]), bits(gw["k_cache"]))
+    assert np.array_equal(bits(gg["v_cache"]), bits(gw["v_cache"]))
+    y = to_np(got)
+    assert np.isfinite(y).all()
+    near = max_abs(y, to_np(want))
+    assert near <= 4e-3, f"against each row's own reads: max-abs {near}"
+    oracle = ko.flash_attn_with_kvcache(to_np(c["q"]), to_np(c["k_cache"]), to_np(c["v_cache"]),
+                                        to_np(c["k"]), to_np(c["v"]), seqlens, -1)[0]
+    err = max_abs(y, oracle)
+    assert err <= ATOL[torch.bfloat16], f"against the oracle: max-abs {err}"
 
 
 def test_shared_prefix_keys_come_from_row_0():
