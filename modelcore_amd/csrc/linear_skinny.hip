@@ -8,11 +8,13 @@
 //
 // Work split. A workgroup owns 16 WAVES consecutive rows of W (outputs n) and a K-range
 // [k0, k0 + K / S); wave w owns rows 16 w .. 16 w + 15 of the tile, and all waves share the
-// activation rows. Two shapes: eight waves (128-row tiles) for wide projections that fill the
-// GPU with S = 1, where sharing one activation tile among more weight rows halves the activation
-// traffic; four waves (64-row tiles) with the K-range split S ways otherwise. With S > 1 the S
-// partial products are summed by a second pass in a fixed order, so results never depend on
-// timing.
+// activation rows. Two shapes: eight waves (128-row tiles) for more than 16 activation rows
+// whenever the 128-row tiles times the K split fit one workgroup per CU (wide projections with
+// S = 1, the others with S chosen for 128-row tiles), where sharing one activation tile among
+// more weight rows halves the activation traffic; four waves (64-row tiles) with the K-range
+// split S ways otherwise. With S > 1 the S partial products are summed by a second pass in a
+// fixed order, so results never depend on timing (nor on the tile shape: a partial's k order is
+// the same).
 //
 // Data path. The K-range is walked in stages of 128: one stage is 16 WAVES rows x 256 bytes of W
 // and 64 rows x 256 bytes of x, brought into LDS by buffer_load ... lds (16 bytes per lane, four
@@ -342,10 +344,14 @@ int check_linear(const void *x, int64_t ldx, const void *w, int64_t m, int64_t n
 }
 
 void launch_linear(const LinParams &P, hipStream_t s) {
-  // Eight waves where 128-row tiles alone fill the GPU and the activation tile is large enough
-  // for its traffic to matter (measured on MI355X, cold weights, 28672 x 4096: 64 rows 49.2 us
-  // against 57.6 with four waves; 16 rows 49.2 against 47.3); four waves otherwise.
-  if (P.S == 1 && P.N >= 192 * 128 && P.M > 16)
+  // Eight waves where the activation tile is large enough for its traffic to matter and the
+  // 128-row tiles (times the K split) fit one workgroup per CU (measured on MI355X, cold weights,
+  // 28672 x 4096: 64 rows 49.2 us against 57.6 with four waves; 16 rows 49.2 against 47.3; with
+  // 64 rows, 6144 x 4096 at S = 4 12.6 us against 14.4 for 64-row tiles at S = 2, 4096 x 14336
+  // at S = 8 22.8 against 25.1 at S = 4); four waves otherwise.
+  const bool wide = P.S == 1 && P.N >= 192 * 128;
+  const bool split128 = P.S > 1 && P.N % 128 == 0 && int64_t(P.N / 128) * P.S <= 256;
+  if (P.M > 16 && (wide || split128))
     launch_skinny<8>(P, s);
   else
     launch_skinny<4>(P, s);

@@ -210,7 +210,9 @@ extern "C" int mcamd_residual_rmsnorm(const void *x, const float *part, int64_t 
   const int64_t chunks = n / 8;
   const dim3 grid{unsigned(m), 1, 1}, block{unsigned(kThreads), 1, 1};
   hipStream_t s = as_stream(stream);
-  if (P.S > kMaxBatchedSplits) {
+  if (P.S > kMaxBatchedSplits && P.S <= 2 * kMaxBatchedSplits && chunks <= 2 * kThreads) {
+    hipLaunchKernelGGL((residual_rmsnorm_kernel<2, 2 * kMaxBatchedSplits>), grid, block, 0, s, P);
+  } else if (P.S > kMaxBatchedSplits) {
     hipLaunchKernelGGL((residual_rmsnorm_kernel<0, 0>), grid, block, 0, s, P);
   } else if (chunks <= kThreads) {
     hipLaunchKernelGGL((residual_rmsnorm_kernel<1, kMaxBatchedSplits>), grid, block, 0, s, P);
