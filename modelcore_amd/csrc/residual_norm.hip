@@ -18,7 +18,9 @@ namespace mcamd {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kMaxBatchedSplits = 4;  // partial counts whose loads are issued together
+// Partial counts whose loads are issued together: up to this many for any row that fits the
+// registers, up to twice as many for rows of at most 2 * kThreads chunks (4096 elements).
+constexpr int kMaxBatchedSplits = 4;
 
 struct ResParams {
   const uint16_t *x, *y;
