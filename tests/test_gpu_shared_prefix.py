@@ -126,3 +126,57 @@ def test_shared_prefix_outside_the_cache_is_refused():
         _call(c, -1, 17)
     with pytest.raises(ValueError):
         _call(c, -1, -1)
+
+
+def test_captured_steps_with_the_prefix_on_the_matrix_cores_replay_the_eager_steps():
+    # Three decode steps with the shared prefix on the matrix cores and the advance folded in,
+    # captured once: every replay (eager work and synchronisations between them) must equal the
+    # eager steps bit for bit, positions included.
+    B, H, H_kv, D, T_max, P, steps = 32, 16, 4, 128, 1200, 1000, 3
+    seqlens = _rows(B, P, 1100, 6)
+    _note("graph, matrix-core prefix", B, P)
+    c = _replicated(seqlens, P, H, H_kv, D, T_max, torch.bfloat16, seed=45)
+    gen = torch.Generator().manual_seed(46)
+    qs = torch.randn(steps, B, 1, H, D, generator=gen).to(torch.bfloat16).to(DEV)
+    ks = torch.randn(steps, B, 1, H_kv, D, generator=gen).to(torch.bfloat16).to(DEV)
+    vs = torch.randn(steps, B, 1, H_kv, D, generator=gen).to(torch.bfloat16).to(DEV)
+    g = {n: t.to(DEV) for n, t in c.items()}
+    outs = [torch.empty(B, 1, H, D, dtype=torch.bfloat16, device=DEV) for _ in range(steps)]
+
+    def run_steps():
+        for s in range(steps):
+            outs[s].copy_(flash_attn.flash_attn_with_kvcache(
+                qs[s], g["k_cache"], g["v_cache"], k=ks[s], v=vs[s],
+                cache_seqlens=g["cache_seqlens"], causal=True, window_size=(-1, 0), advance=1,
+                shared_prefix=P))
+
+    def reset():
+        g["k_cache"].copy_(c["k_cache"])
+        g["v_cache"].copy_(c["v_cache"])
+        g["cache_seqlens"].copy_(c["cache_seqlens"])
+
+    run_steps()  # warm-up (workspace sized)
+    reset()
+    run_steps()
+    torch.cuda.synchronize()
+    eager = [bits(o) for o in outs]
+    eager_k = bits(g["k_cache"])
+    assert g["cache_seqlens"].tolist() == [p + steps for p in seqlens]
+    reset()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run_steps()
+    for rep in range(3):
+        reset()
+        torch.cuda.synchronize()
+        for o in outs:
+            o.fill_(0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert g["cache_seqlens"].tolist() == [p + steps for p in seqlens], f"replay {rep}"
+        assert np.array_equal(bits(g["k_cache"]), eager_k), f"replay {rep}: cache"
+        for s in range(steps):
+            assert np.array_equal(bits(outs[s]), eager[s]), f"replay {rep}, step {s}"
+        run_steps()
+        torch.cuda.synchronize()
