@@ -37,6 +37,9 @@ HIPCC_FLAGS = [
     "-Wall",
     "-Wno-unused-command-line-argument",
     "-I", str(REPO_DIR / "include"),
+    # Kernel arguments: the first 14 dwords of scalar (not aggregate) arguments arrive in SGPRs
+    # at dispatch instead of through a load from the kernel-argument buffer.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

@@ -104,8 +104,21 @@ __device__ __forceinline__ uint16_t silu_mul_bf16(float gate, float up) {
   return to_bf16(a * u);
 }
 
+// The leading arguments repeat the fields of P that the tile set-up needs, so that they arrive
+// preloaded in SGPRs at dispatch (the library is built with kernarg preloading, which covers
+// scalar arguments only) rather than through a load from the kernel-argument buffer.
 template <int WAVES, int MB>  // MB blocks of 16 activation rows: M <= 16 MB
-__global__ __launch_bounds__(64 * WAVES, 1) void linear_skinny_kernel(LinParams P) {
+__global__ __launch_bounds__(64 * WAVES, 1) void linear_skinny_kernel(
+    const uint16_t *a_x, const uint16_t *a_w, int64_t a_ldx, int a_M, int a_N, int a_K, int a_S,
+    int a_w_tiled, LinParams P) {
+  P.x = a_x;
+  P.w = a_w;
+  P.ldx = a_ldx;
+  P.M = a_M;
+  P.N = a_N;
+  P.K = a_K;
+  P.S = a_S;
+  P.w_tiled = a_w_tiled;
   constexpr int kRows = 16 * WAVES;         // rows of W per workgroup
   constexpr int kRing = WAVES == 8 ? 3 : 4; // LDS stages
   constexpr int kStageW = kRows * KC;       // elements of one W stage
@@ -291,13 +304,13 @@ void launch_skinny(const LinParams &P, hipStream_t s) {
   const dim3 grid(unsigned((P.N + 16 * WAVES - 1) / (16 * WAVES)), unsigned(P.S));
   const dim3 block(64 * WAVES);
   if (P.M <= 16)
-    hipLaunchKernelGGL((linear_skinny_kernel<WAVES, 1>), grid, block, 0, s, P);
+    hipLaunchKernelGGL((linear_skinny_kernel<WAVES, 1>), grid, block, 0, s, P.x, P.w, P.ldx, P.M, P.N, P.K, P.S, P.w_tiled, P);
   else if (P.M <= 32)
-    hipLaunchKernelGGL((linear_skinny_kernel<WAVES, 2>), grid, block, 0, s, P);
+    hipLaunchKernelGGL((linear_skinny_kernel<WAVES, 2>), grid, block, 0, s, P.x, P.w, P.ldx, P.M, P.N, P.K, P.S, P.w_tiled, P);
   else if (P.M <= 48)
-    hipLaunchKernelGGL((linear_skinny_kernel<WAVES, 3>), grid, block, 0, s, P);
+    hipLaunchKernelGGL((linear_skinny_kernel<WAVES, 3>), grid, block, 0, s, P.x, P.w, P.ldx, P.M, P.N, P.K, P.S, P.w_tiled, P);
   else
-    hipLaunchKernelGGL((linear_skinny_kernel<WAVES, 4>), grid, block, 0, s, P);
+    hipLaunchKernelGGL((linear_skinny_kernel<WAVES, 4>), grid, block, 0, s, P.x, P.w, P.ldx, P.M, P.N, P.K, P.S, P.w_tiled, P);
 }
 
 }  // namespace

@@ -54,8 +54,22 @@ __device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
 // MAXS > 0 (at most MAXS partials): the partial loads of all the thread's chunks are issued
 // before the first is summed, so they cost one memory latency, not one per partial and chunk;
 // MAXS = 0: any number of partials, loaded one after the other.
+// The fields of ResParams come as separate scalar arguments: the library is built with kernarg
+// preloading, so all fourteen dwords of them arrive in SGPRs at dispatch.
 template <int CPT, int MAXS>
-__global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(ResParams P) {
+__global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(
+    const uint16_t *a_x, const uint16_t *a_y, const float *a_part, uint16_t *a_x_out,
+    uint16_t *a_h_out, int a_M, int a_N, int a_S, float a_eps) {
+  ResParams P;
+  P.x = a_x;
+  P.y = a_y;
+  P.part = a_part;
+  P.x_out = a_x_out;
+  P.h_out = a_h_out;
+  P.M = a_M;
+  P.N = a_N;
+  P.S = a_S;
+  P.eps = a_eps;
   __shared__ float wsum[kThreads / 64];
   const int m = blockIdx.x;
   const int chunks = P.N / 8;
@@ -213,17 +227,17 @@ extern "C" int mcamd_residual_rmsnorm(const void *x, const float *part, int64_t 
   const dim3 grid{unsigned(m), 1, 1}, block{unsigned(kThreads), 1, 1};
   hipStream_t s = as_stream(stream);
   if (P.S > kMaxBatchedSplits && P.S <= 2 * kMaxBatchedSplits && chunks <= 2 * kThreads) {
-    hipLaunchKernelGGL((residual_rmsnorm_kernel<2, 2 * kMaxBatchedSplits>), grid, block, 0, s, P);
+    hipLaunchKernelGGL((residual_rmsnorm_kernel<2, 2 * kMaxBatchedSplits>), grid, block, 0, s, P.x, P.y, P.part, P.x_out, P.h_out, P.M, P.N, P.S, P.eps);
   } else if (P.S > kMaxBatchedSplits) {
-    hipLaunchKernelGGL((residual_rmsnorm_kernel<0, 0>), grid, block, 0, s, P);
+    hipLaunchKernelGGL((residual_rmsnorm_kernel<0, 0>), grid, block, 0, s, P.x, P.y, P.part, P.x_out, P.h_out, P.M, P.N, P.S, P.eps);
   } else if (chunks <= kThreads) {
-    hipLaunchKernelGGL((residual_rmsnorm_kernel<1, kMaxBatchedSplits>), grid, block, 0, s, P);
+    hipLaunchKernelGGL((residual_rmsnorm_kernel<1, kMaxBatchedSplits>), grid, block, 0, s, P.x, P.y, P.part, P.x_out, P.h_out, P.M, P.N, P.S, P.eps);
   } else if (chunks <= 2 * kThreads) {
-    hipLaunchKernelGGL((residual_rmsnorm_kernel<2, kMaxBatchedSplits>), grid, block, 0, s, P);
+    hipLaunchKernelGGL((residual_rmsnorm_kernel<2, kMaxBatchedSplits>), grid, block, 0, s, P.x, P.y, P.part, P.x_out, P.h_out, P.M, P.N, P.S, P.eps);
   } else if (chunks <= 4 * kThreads) {
-    hipLaunchKernelGGL((residual_rmsnorm_kernel<4, kMaxBatchedSplits>), grid, block, 0, s, P);
+    hipLaunchKernelGGL((residual_rmsnorm_kernel<4, kMaxBatchedSplits>), grid, block, 0, s, P.x, P.y, P.part, P.x_out, P.h_out, P.M, P.N, P.S, P.eps);
   } else {
-    hipLaunchKernelGGL((residual_rmsnorm_kernel<0, kMaxBatchedSplits>), grid, block, 0, s, P);
+    hipLaunchKernelGGL((residual_rmsnorm_kernel<0, kMaxBatchedSplits>), grid, block, 0, s, P.x, P.y, P.part, P.x_out, P.h_out, P.M, P.N, P.S, P.eps);
   }
   return launch_status("residual_rmsnorm");
 }
