@@ -199,15 +199,17 @@ __device__ __forceinline__ void keep_tile(const Tile &t, float &anchor) {
                "v"(__builtin_bit_cast(u32x4, t.v[2])), "v"(__builtin_bit_cast(u32x4, t.v[3])));
 }
 
-// Keys of row b (the range [lo, pos]), or 0 for a row whose position is outside the cache.
-__device__ __forceinline__ int row_keys(const FusedParams &P, int b, int &lo) {
-  const int pos = P.seqlens[b];
+// Keys of a row at position pos (the range [lo, pos]), or 0 for a position outside the cache.
+__device__ __forceinline__ int row_keys_at(const FusedParams &P, int pos, int &lo) {
   if (pos < 0 || pos >= P.T_max) {
     lo = 0;
     return 0;
   }
   lo = max(key_lo(pos, P.window), P.lo_floor);
   return max(pos - lo + 1, 0);
+}
+__device__ __forceinline__ int row_keys(const FusedParams &P, int b, int &lo) {
+  return row_keys_at(P, P.seqlens[b], lo);
 }
 
 // Slots a unit of a row with nk keys takes in the work split: kSegCost lead slots that hold no
@@ -291,13 +293,13 @@ struct WaveAcc {
 
 
 // This workgroup's share of the slots: total T, active workgroups NG = min(n_groups, T), the
-// range [start, end), and the row b holding `start` with Pb its first slot. One read of
-// cache_seqlens when B <= 64.
-__device__ void locate(const FusedParams &P, int g, int lane, int64_t &T, int &NG, int64_t &start,
-                       int64_t &end, int &b, int64_t &Pb) {
+// range [start, end), and the row b holding `start` with Pb its first slot. With B <= 64 the
+// rows' positions come in pos_lane (lane b holds row b's), read by the caller.
+__device__ void locate(const FusedParams &P, int g, int lane, int pos_lane, int64_t &T, int &NG,
+                       int64_t &start, int64_t &end, int &b, int64_t &Pb) {
   if (P.scan32) {
     int lo;
-    const int nk = lane < P.B ? row_keys(P, lane, lo) : 0;
+    const int nk = lane < P.B ? row_keys_at(P, pos_lane, lo) : 0;
     const int tot = unit_span(nk) * P.n_units;
     const int incl = scan_incl_i32(tot);
     T = __builtin_amdgcn_readlane(incl, 63);
@@ -312,7 +314,7 @@ __device__ void locate(const FusedParams &P, int g, int lane, int64_t &T, int &N
   }
   if (P.B <= 64) {
     int lo;
-    const int nk = lane < P.B ? row_keys(P, lane, lo) : 0;
+    const int nk = lane < P.B ? row_keys_at(P, pos_lane, lo) : 0;
     const int64_t tot = int64_t(unit_span(nk)) * P.n_units;
     const int64_t incl = scan_incl_i64(tot, lane);
     T = shfl_i64(incl, 63);
@@ -371,11 +373,19 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(
   const int r = lane >> 4;  // KV head within the unit's group of four
   const int c = lane & 15;  // 16-byte column of the head row
 
+  // With at most 64 rows, the positions are read once, first thing (lane b holds row b's): the
+  // check of rows outside the cache, the work split and each segment's row take them from here,
+  // so the work split does not wait for a second read of cache_seqlens.
+  const bool few_rows = P.B <= 64;
+  const int pos_lane = few_rows && lane < P.B ? P.seqlens[lane] : 0;
+  auto row_pos = [&](int row) {
+    return few_rows ? __builtin_amdgcn_readlane(pos_lane, row) : P.seqlens[row];
+  };
   // Rows outside the cache: NaN output and a descriptor of no segments for each of their units
   // (so the merge pass need not read cache_seqlens), written by workgroup b % n_groups.
   for (int b = g; b < P.B; b += P.n_groups) {
     int lo;
-    if (row_keys(P, b, lo) == 0) {
+    if (row_keys_at(P, row_pos(b), lo) == 0) {
       for (int i = threadIdx.x; i < P.H * D; i += 64 * NW) P.out[int64_t(b) * P.H * D + i] = 0x7fc0;
       for (int u = threadIdx.x; u < P.n_units; u += 64 * NW)
         P.desc[int64_t(b) * P.n_units + u] = make_int2(0, 0);
@@ -386,7 +396,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(
   // key's (a range of lead slots alone holds no key of the unit and writes nothing for it).
   int64_t T, start = 0, end = 0, Pb = 0;
   int NG, b = 0;
-  locate(P, g, lane, T, NG, start, end, b, Pb);
+  locate(P, g, lane, pos_lane, T, NG, start, end, b, Pb);
   if (g >= NG) return;
 
   const bool fuse_new = P.k_new != nullptr;
@@ -394,7 +404,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(
   int64_t x = start;
   while (x < end) {
     int lo;
-    const int nk = row_keys(P, b, lo);
+    const int nk = row_keys_at(P, row_pos(b), lo);
     const int span = unit_span(nk);
     const int pos = lo + nk - 1;
     const int64_t off = x - Pb;
@@ -656,7 +666,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(
       int lo2;
       do {
         ++b;
-      } while (b < P.B && row_keys(P, b, lo2) == 0);
+      } while (b < P.B && row_keys_at(P, row_pos(b), lo2) == 0);
     }
   }
 }
