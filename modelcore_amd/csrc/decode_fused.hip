@@ -707,7 +707,9 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
   const int hc = unit - kg * P.n_hc;
   const int kvh = kg * KG + hr / GM;
   const int hh = hr % GM;
-  if (P.advance != 0 && unit == 0 && hr == 0 && lane == 0) P.adv_seqlens[b] += P.advance;
+  // An atomic add whose result is not used: the wave does not wait for a read of the position
+  // before its own loads (one wave and lane per row adds, so it is a plain increment).
+  if (P.advance != 0 && unit == 0 && hr == 0 && lane == 0) atomicAdd(P.adv_seqlens + b, P.advance);
   if (kvh >= P.H_kv || hh >= min(GM, P.G - hc * GM)) return;
   const float *bucket = P.part + int64_t(ug) * kBucket * kPart;
   auto seg_at = [&](int j, int g_first) {
@@ -732,6 +734,14 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
       pml[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * hr);
       pv[k] = *reinterpret_cast<const float2 *>(ps + hr * D + 2 * lane);
     }
+  }
+  // The loads above stay ahead of the branch below: the compiler would otherwise sink them past
+  // it and issue them only once the descriptor is back (two memory round trips, not one).
+#pragma unroll
+  for (int k = 0; k < SPEC; ++k) asm volatile("" ::"v"(ml[k]), "v"(v[k]));
+  if constexpr (PRE) {
+#pragma unroll
+    for (int k = 0; k < NP; ++k) asm volatile("" ::"v"(pml[k]), "v"(pv[k]));
   }
   const int g_first = d.x, nseg = d.y;
   // No keys (a row outside the cache: NaN written), or a unit written directly.
