@@ -79,10 +79,24 @@ struct EpiParams {
   int part_S;
 };
 
+// The leading arguments repeat the fields of P that the first loads need (the row's position,
+// then its source row), so that they arrive preloaded in SGPRs at dispatch (the library is
+// built with kernarg preloading, which covers scalar arguments only).
 template <bool BF16>
-__global__ __launch_bounds__(64 * kWavesPerBlock) void qk_epilogue_kernel(EpiParams P) {
+__global__ __launch_bounds__(64 * kWavesPerBlock) void qk_epilogue_kernel(
+    const int32_t *a_seqlens, const float *a_part, int64_t a_part_tok, int64_t a_n_tokens,
+    int a_n_items, int a_t_new, int a_D, int a_H, int a_H_kv, EpiParams P) {
   // Every product and sum is rounded on its own, as the separate torch kernels do.
 #pragma clang fp contract(off)
+  P.seqlens = a_seqlens;
+  P.part = a_part;
+  P.part_tok = a_part_tok;
+  P.n_tokens = a_n_tokens;
+  P.n_items = a_n_items;
+  P.t_new = a_t_new;
+  P.D = a_D;
+  P.H = a_H;
+  P.H_kv = a_H_kv;
   typedef Elem<BF16> E;
   typedef typename E::T T;
   const int lane = threadIdx.x & 63;
@@ -234,10 +248,12 @@ extern "C" int mcamd_qk_rope_norm_append(const void *q, int64_t q_token_stride, 
   if (blocks > 0x7fffffff) return fail(MCAMD_EUNSUPPORTED, "qk_rope_norm_append: grid too large");
   if (dtype == MCAMD_BF16)
     hipLaunchKernelGGL(qk_epilogue_kernel<true>, dim3(unsigned(blocks)), dim3(64 * kWavesPerBlock),
-                       0, as_stream(stream), P);
+                       0, as_stream(stream), P.seqlens, P.part, P.part_tok, P.n_tokens,
+                       P.n_items, P.t_new, P.D, P.H, P.H_kv, P);
   else
     hipLaunchKernelGGL(qk_epilogue_kernel<false>, dim3(unsigned(blocks)),
-                       dim3(64 * kWavesPerBlock), 0, as_stream(stream), P);
+                       dim3(64 * kWavesPerBlock), 0, as_stream(stream), P.seqlens, P.part, P.part_tok, P.n_tokens,
+                       P.n_items, P.t_new, P.D, P.H, P.H_kv, P);
   return launch_status("qk_rope_norm_append");
 }
 
@@ -297,6 +313,7 @@ extern "C" int mcamd_qk_rope_norm_append_partials(
   if (blocks > 0x7fffffff)
     return fail(MCAMD_EUNSUPPORTED, "qk_rope_norm_append_partials: grid too large");
   hipLaunchKernelGGL(qk_epilogue_kernel<true>, dim3(unsigned(blocks)), dim3(64 * kWavesPerBlock),
-                     0, as_stream(stream), P);
+                     0, as_stream(stream), P.seqlens, P.part, P.part_tok, P.n_tokens,
+                       P.n_items, P.t_new, P.D, P.H, P.H_kv, P);
   return launch_status("qk_rope_norm_append_partials");
 }
