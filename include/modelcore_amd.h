@@ -2,8 +2,11 @@
  * modelcore_amd: C ABI of the MI355X (gfx950) KV-cache and cached-attention path.
  *
  * Every entry point takes plain device pointers, element counts and a hipStream_t passed as
- * `void *stream` (NULL = the null stream). Nothing here allocates device memory, synchronises
- * the host or keeps mutable global state: work is enqueued on `stream` and the call returns.
+ * `void *stream` (NULL = the null stream). Nothing here allocates device memory or synchronises
+ * the host: work is enqueued on `stream` and the call returns. The library keeps two caches of
+ * per-device facts, both safe to use from several threads: the compute-unit count of each device
+ * (queried once, atomically published) and, for mcamd_flash_attn_with_kvcache_noalloc, the
+ * address of its static scratch array on each device (looked up once, under a mutex).
  * Each function returns 0 on success or a negative MCAMD_E* code; mcamd_last_error() then
  * describes the failure (thread-local, valid until the next call on the same thread).
  *
@@ -122,7 +125,9 @@ int mcamd_flash_attn_with_kvcache(const void *q, const void *k, const void *v,
  *    other way). Otherwise the decode pass reads them from row 0 itself: the same values in the
  *    same order, so the same results bit for bit, with the rows' repeated reads of one row's
  *    lines served by the caches. Other paths read each row's own copy. A statement that does not
- *    hold gives rows row 0's keys below shared_prefix.
+ *    hold gives rows row 0's keys below shared_prefix; on the matrix-core way, a row whose
+ *    position lies below shared_prefix is moreover treated as outside the cache (NaN output, no
+ *    append). The Python operator's checked mode raises for such a row before launching.
  * With both 0 this is exactly mcamd_flash_attn_with_kvcache; otherwise the cache contents are
  * bit-identical to that call's (followed by the separate advance) whenever the statement holds,
  * and the outputs as described above.

@@ -37,8 +37,11 @@ HIPCC_FLAGS = [
     "-Wall",
     "-Wno-unused-command-line-argument",
     "-I", str(REPO_DIR / "include"),
-    # Kernel arguments: the first 14 dwords of scalar (not aggregate) arguments arrive in SGPRs
-    # at dispatch instead of through a load from the kernel-argument buffer.
+    # Kernel arguments: LLVM preloads up to the first 16 kernel *arguments* (the count is of
+    # arguments, not dwords) into SGPRs at dispatch instead of loading them from the
+    # kernel-argument buffer. It stops at the first aggregate (struct) argument or when the free
+    # user SGPRs run out, so on gfx950 at most 14 dwords of leading scalar arguments arrive this
+    # way; the kernels that care put the fields they need first as leading scalar arguments.
     "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 

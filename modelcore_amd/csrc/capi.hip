@@ -67,7 +67,7 @@ extern "C" size_t mcamd_attn_workspace_bytes(int64_t batch, int64_t t_new, int64
   // Room for the shared-prefix partials too, where the fused decode can take a shared prefix on
   // the matrix cores; a workspace of decode_workspace_bytes() alone still serves every call.
   return decode_workspace_bytes(batch, n_head, n_kv_head, head_dim, t_max, window) +
-         decode_prefix_bytes(batch, n_head, n_kv_head, head_dim, window);
+         decode_prefix_bytes(batch, n_head, n_kv_head, head_dim, t_max, window);
 }
 
 extern "C" int mcamd_decode_attention(const void *q, const void *k_cache, const void *v_cache,

@@ -52,6 +52,8 @@
 //    lines served by L2 and the memory-side cache instead of HBM.
 #include "kernels.h"
 
+#include <atomic>
+
 #include <cmath>
 
 namespace mcamd {
@@ -347,9 +349,9 @@ __device__ __forceinline__ int xcd_major(int id, int n) {
 // NT: K/V loads non-temporal (calls too large to stay in the memory-side cache) or with the
 // default policy (small calls, whose K/V a KV-sharing layer may read again right after).
 // The leading arguments repeat the fields of P that the first instructions need (the position
-// scan, then the q and K/V addresses). The library is built with kernarg preloading, which
-// hands a kernel's first 14 argument dwords over in SGPRs at dispatch: scalar arguments only,
-// hence the copies. The scan then starts without waiting for a kernel-argument load from memory
+// scan, then the q and K/V addresses). The library is built with kernarg preloading (up to 16
+// leading arguments, as many as fit the 14 free user SGPRs, stopping at the first aggregate):
+// scalar arguments only, hence the copies. The scan then starts without waiting for a kernel-argument load from memory
 // (measured: mixed-window step 0.394 -> 0.387 ms, decode call +0.3%, four paired runs).
 template <bool NT>
 __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(
@@ -778,18 +780,19 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
                                 2 * lane) = pack_bf16(t0 * inv, t1 * inv);
 }
 
-// Number of compute units of the current device (queried once per device).
+// Number of compute units of the current device, queried once per device. Threads that race on
+// the first query each store the same value; the atomics make that well-defined.
 int device_cus() {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 }  // namespace
@@ -808,10 +811,12 @@ size_t decode_fused_partial_bytes(int64_t batch, int64_t n_head, int64_t n_kv_he
 }
 
 size_t decode_prefix_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
-                           int64_t window) {
+                           int64_t t_max, int64_t window) {
   // Worth it for many queries per KV head (rows x query heads fill most of the matrix-core
-  // kernel's 256 pairs) and without a window (its keys would then differ per row).
-  if (head_dim != D || window >= 0 || n_kv_head <= 0 || batch * (n_head / n_kv_head) < 64)
+  // kernel's 256 pairs) and without a window (its keys would then differ per row); possible only
+  // for geometries the matrix-core kernel takes.
+  if (head_dim != D || window >= 0 || n_kv_head <= 0 || batch * (n_head / n_kv_head) < 64 ||
+      !prefill_mfma_geometry_ok(n_head, n_kv_head, t_max))
     return 0;
   const int64_t units = batch * decode_fused_units(n_head, n_kv_head);
   return size_t(units * kPrefixMaxSplits * kPart * 4);
@@ -868,7 +873,8 @@ int launch_decode_fused(const AttnArgs &a) {
   P.n_pre = 0;
   const size_t base_ws =
       decode_workspace_bytes(a.batch, a.n_head, a.n_kv_head, a.head_dim, a.t_max, a.window);
-  const size_t pre_ws = decode_prefix_bytes(a.batch, a.n_head, a.n_kv_head, a.head_dim, a.window);
+  const size_t pre_ws =
+      decode_prefix_bytes(a.batch, a.n_head, a.n_kv_head, a.head_dim, a.t_max, a.window);
   if (pre_ws > 0 && a.shared_prefix >= kPrefixMinKeys && a.workspace_bytes >= base_ws + pre_ws) {
     P.n_pre = int(std::min<int64_t>(kPrefixMaxSplits, a.shared_prefix / kPrefixKeysPerSplit));
     P.lo_floor = int(a.shared_prefix);

@@ -77,9 +77,13 @@ struct PrefixArgs {
 };
 int launch_prefix_partials(const PrefixArgs &a);
 // Bytes of workspace past decode_workspace_bytes() for those partials (0 where the fused decode
-// never takes the prefix on the matrix cores).
+// never takes the prefix on the matrix cores: such calls read row 0's keys in the streaming pass).
 size_t decode_prefix_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
-                           int64_t window);
+                           int64_t t_max, int64_t window);
+// Whether the matrix-core kernel takes a (query heads, KV heads, T_max) geometry at all: at most
+// 256 query heads per KV head (one workgroup's pairs) and one (row, KV head)'s cache addressable
+// with 32-bit byte offsets.
+bool prefill_mfma_geometry_ok(int64_t n_head, int64_t n_kv_head, int64_t t_max);
 
 // The fused bf16 / head_dim 128 decode (append + split-K + merge in one launch).
 bool decode_fused_supported(const AttnArgs &a);

@@ -80,8 +80,10 @@ int run(const AppendArgs &a, int64_t row_bytes) {
     clear_error();
     return MCAMD_OK;
   }
-  if (a.t_new * upr >= (int64_t(1) << 31))
-    return fail(MCAMD_EUNSUPPORTED, "kv_append: more than 2^31 units in one row's new tokens");
+  // The kernel's int unit indices reach the row's unit count plus one block's reach.
+  if (a.t_new * upr > (int64_t(1) << 31) - 1 - int64_t(kThreads) * kUnroll)
+    return fail(MCAMD_EUNSUPPORTED, "kv_append: too many units in one row's new tokens for 32-bit "
+                                    "indices");
   const int64_t per_block = int64_t(kThreads) * kUnroll;
   const unsigned blocks = unsigned((a.t_new * upr + per_block - 1) / per_block);
   int shift = 0;

@@ -490,11 +490,16 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
 
 }  // namespace
 
-bool prefill_mfma_supported(const AttnArgs &a) {
+bool prefill_mfma_geometry_ok(int64_t n_head, int64_t n_kv_head, int64_t t_max) {
+  if (n_kv_head <= 0 || n_head < n_kv_head || t_max <= 0) return false;
   // Byte offsets within one (row, KV head) must fit the 32-bit buffer offsets.
-  const int64_t extent = ((a.t_max - 1) * a.n_kv_head * D + D) * 2;
-  return a.dtype == MCAMD_BF16 && a.head_dim == D && a.n_head / a.n_kv_head <= kPairs &&
-         a.n_kv_head < 65536 && extent < (int64_t(1) << 31);
+  const int64_t extent = ((t_max - 1) * n_kv_head * D + D) * 2;
+  return n_head / n_kv_head <= kPairs && n_kv_head < 65536 && extent < (int64_t(1) << 31);
+}
+
+bool prefill_mfma_supported(const AttnArgs &a) {
+  return a.dtype == MCAMD_BF16 && a.head_dim == D &&
+         prefill_mfma_geometry_ok(a.n_head, a.n_kv_head, a.t_max);
 }
 
 int launch_prefill_mfma(const AttnArgs &a) {

@@ -55,7 +55,8 @@ __device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
 // before the first is summed, so they cost one memory latency, not one per partial and chunk;
 // MAXS = 0: any number of partials, loaded one after the other.
 // The fields of ResParams come as separate scalar arguments: the library is built with kernarg
-// preloading, so all fourteen dwords of them arrive in SGPRs at dispatch.
+// preloading (leading scalar arguments, as many as fit the 14 free user SGPRs), and these
+// fourteen dwords all arrive in SGPRs at dispatch.
 template <int CPT, int MAXS>
 __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(
     const uint16_t *a_x, const uint16_t *a_y, const float *a_part, uint16_t *a_x_out,

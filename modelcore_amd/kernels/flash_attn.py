@@ -71,7 +71,7 @@ def set_checked(enabled: bool):
     CHECK_POSITIONS = bool(enabled)
 
 
-def _check_positions(seqlens, T_new, T_max):
+def _check_positions(seqlens, T_new, T_max, shared_prefix=0):
     if torch.cuda.is_current_stream_capturing():
         raise RuntimeError("flash_attn_with_kvcache: checked mode reads cache_seqlens on the host "
                            "and cannot run under graph capture; call set_checked(False) first")
@@ -79,6 +79,10 @@ def _check_positions(seqlens, T_new, T_max):
     if lo < 0 or hi + T_new > T_max:
         raise IndexError(f"flash_attn_with_kvcache: positions [{lo}, {hi + T_new}) of the new "
                          f"tokens fall outside the cache of {T_max} positions")
+    # The shared-prefix statement includes that every new token lands at or past the prefix.
+    if lo < shared_prefix:
+        raise ValueError(f"flash_attn_with_kvcache: shared_prefix {shared_prefix} past the "
+                         f"position {lo} of a row's new token")
 
 
 def hip_load_error():
@@ -191,7 +195,7 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
         raise ValueError("advance needs cache_seqlens itself to be contiguous (it is updated in "
                          "place)")
     if CHECK_POSITIONS and B > 0:
-        _check_positions(seqlens, T_new, T_max)
+        _check_positions(seqlens, T_new, T_max, shared_prefix)
     q = q.contiguous()
     if k is not None:
         k, v = k.contiguous(), v.contiguous()

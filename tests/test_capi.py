@@ -78,6 +78,34 @@ def test_workspace_size_follows_the_split_count():
     assert lib.mcamd_attn_workspace_bytes(B, 7, H, 4, D, T_max, -1) == 0  # prefill needs none
 
 
+def _base_workspace(B, H, H_kv, D, T_max, window=-1):
+    """The decode partials of the general and fused kernels (bf16, head_dim 128), rounded up."""
+    n_splits = -(-(T_max if window < 0 else min(T_max, window + 1)) // 256)
+    general = B * H * n_splits * (D + 2) * 4
+    units = B * -(-H_kv // 4) * -(-(H // H_kv) // 4)
+    fused = (16 * units + 1024 + units) * (16 * (D + 2)) * 4 + units * 8
+    return -(-max(general, fused) // 256) * 256, units
+
+
+def test_shared_prefix_slots_only_where_the_matrix_core_kernel_takes_the_geometry():
+    """The shared prompt prefix goes to the matrix-core kernel only for geometries that kernel
+    takes: at most 256 query heads per KV head, and one (row, KV head)'s cache within 32-bit byte
+    offsets. Elsewhere the workspace holds no prefix slots and the decode pass reads row 0."""
+    lib = _ext.lib()
+    D = 128
+    prefix_slots = lambda units: units * 16 * (16 * (D + 2)) * 4  # noqa: E731
+    # 16 KV heads at 2^16 positions: offsets fit; at 2^20 they do not
+    for T_max, takes in ((1 << 16, True), (1 << 20, False)):
+        base, units = _base_workspace(64, 32, 16, D, T_max)
+        got = lib.mcamd_attn_workspace_bytes(64, 1, 32, 16, D, T_max, -1)
+        assert got == base + (prefix_slots(units) if takes else 0), T_max
+    # 256 query heads per KV head fill one workgroup's pairs; 512 would not fit
+    for H, takes in ((256, True), (512, False)):
+        base, units = _base_workspace(1, H, 1, D, 1024)
+        got = lib.mcamd_attn_workspace_bytes(1, 1, H, 1, D, 1024, -1)
+        assert got == base + (prefix_slots(units) if takes else 0), H
+
+
 def test_a_missing_library_raises_with_its_reason(monkeypatch, tmp_path):
     monkeypatch.setattr(_ext, "LIB_PATH", tmp_path / "absent.so")
     _ext.reload()

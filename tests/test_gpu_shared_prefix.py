@@ -67,6 +67,9 @@ READ_CASES = [
     (torch.bfloat16, 700, [700, 705, 1200, 900], 16, 4, 128, 1300, 64),    # windows: inside, across
     (torch.bfloat16, 700, [700, 705, 1200, 900], 16, 4, 128, 1300, 300),   # and past the prefix
     (torch.bfloat16, 2048, [2048] + _rows(63, 2048, 2560, 5), 32, 8, 128, 2560, 600),
+    # 512 query heads per KV head: more than the matrix-core kernel's 256 pairs per workgroup,
+    # so the decode pass reads the prefix from row 0 even though rows x heads >= 64
+    (torch.bfloat16, 600, [600, 700], 512, 1, 128, 800, -1),
     (torch.bfloat16, 64, [64, 80, 64], 8, 2, 64, 128, -1),                 # general path: ignored
     (torch.float32, 64, [64, 80, 64], 8, 2, 128, 128, -1),
 ]
