@@ -10,9 +10,13 @@ before timing starts; the K timed steps run as one HIP graph replay.
 
 Prints one JSON line: tokens/s (32 tokens per step), the roofline of the decode attention
 (algorithmic bytes over its event-timed duration against 8 TB/s), and the reference's CPU
-fallback timed on this host's cores on the same workload.
+fallback timed on this host's cores on the same workload. Unless --decode-only, the line also
+carries a `subsystems` object with the other workloads of the path, each with its own roofline
+and CPU baseline: the chunked prefill (attention MFMA utilisation and append GB/s), the
+mixed-window stack's decode step and the replication of a prompt cache into 64 rows (the same
+measurements as --workload prefill / mixed / replicate, with fixed step counts).
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline] [--decode-only]
 
 The roofline figure times the decode call alone, ROOF_LAUNCHES launches at the drawn lengths
 (seed 0), whatever --steps and --warmup are, so that its bytes -- and the HBM traffic the
@@ -67,6 +71,9 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="default workload: time the decode microbench only, without the "
+                         "prefill, mixed-window and replication objects")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
     ap.add_argument("--library-gemm", action="store_true",
                     help="sample workload: run the decode projections through F.linear (the "
@@ -371,36 +378,34 @@ def bench_prefill(args):
                    "bytes_per_launch": append_bytes // n_chunks},
     }
     if not args.no_cpu_baseline:
+        log("CPU baseline: the whole chunked prefill on host cores")
         result["cpu_baseline"] = cpu_prefill_baseline(q, k, v)
-    print(json.dumps(result), flush=True)
+    return result
 
 
-def cpu_prefill_baseline(q, k, v, budget_s=15.0):
-    """The restated reference fallback (append + masked SDPA with GQA, torch CPU) on one chunk of
-    the workload at the middle of the prompt (prefix 8192: the mean attention cost of a chunk)."""
+def cpu_prefill_baseline(q, k, v):
+    """The restated reference fallback (append + masked SDPA with GQA, torch CPU) on the whole
+    workload: the same 32 chunks of all 8 rows, appended and attended in order, timed once
+    (about 15 s on 16 cores)."""
     import torch
     from oracle import sdpa_fallback
 
     cores = host_cores()
     torch.set_num_threads(cores)
-    a = PF_T // 2
-    end = a + PF_C
-    qc = q[:, a:end].cpu()
-    kn, vn = k[:, a:end].cpu(), v[:, a:end].cpu()
-    kc = torch.zeros(PF_B, end, PF_HKV, D, dtype=torch.bfloat16)
+    qc, kn, vn = q.cpu(), k.cpu(), v.cpu()
+    kc = torch.zeros(PF_B, PF_T, PF_HKV, D, dtype=torch.bfloat16)
     vc = torch.zeros_like(kc)
-    kc[:, :a], vc[:, :a] = k[:, :a].cpu(), v[:, :a].cpu()
-    pos = torch.full((PF_B,), a, dtype=torch.int32)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
-        t0 = time.perf_counter()
-        sdpa_fallback.flash_attn_with_kvcache(qc, kc, vc, kn, vn, pos, (-1, 0))
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    return {"value": round(PF_B * PF_C / med, 1), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"one 512-token chunk of all 8 rows at prefix 8192 (mid-prompt), median of "
-                      f"{len(times)} runs; torch CPU SDPA restatement of the reference fallback"}
+    t0 = time.perf_counter()
+    for c in range(PF_T // PF_C):
+        a, e = c * PF_C, (c + 1) * PF_C
+        pos = torch.full((PF_B,), a, dtype=torch.int32)
+        sdpa_fallback.flash_attn_with_kvcache(qc[:, a:e], kc, vc, kn[:, a:e], vn[:, a:e], pos,
+                                              (-1, 0))
+    dt = time.perf_counter() - t0
+    return {"value": round(PF_B * PF_T / dt, 1), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"the whole workload (8 rows x 16384 tokens, 32 chunks of 512, append + "
+                      f"attention per chunk), one pass of {dt:.1f} s; torch CPU SDPA restatement "
+                      f"of the reference fallback"}
 
 
 RP_SLOTS, RP_P, RP_ROWS, RP_T, RP_HKV = 32, 2048, 64, 2560, 8
@@ -458,8 +463,9 @@ def bench_replicate(args):
                      "traffic": None, "bytes_per_launch": nbytes},
     }
     if not args.no_cpu_baseline:
+        log("CPU baseline: the replication's broadcast copy on host cores")
         result["cpu_baseline"] = cpu_replicate_baseline(src)
-    print(json.dumps(result), flush=True)
+    return result
 
 
 def cpu_replicate_baseline(src, budget_s=10.0):
@@ -580,39 +586,48 @@ def bench_mixed(args):
                      "bytes_per_step": int(step_bytes)},
     }
     if not args.no_cpu_baseline:
-        log("CPU baseline: one window-1024 call and one global call of the stack on host cores")
-        result["cpu_baseline"] = cpu_mixed_baseline(cache, qs[0, 0], ks[0, 0], vs[0, 0], windows)
-    print(json.dumps(result), flush=True)
+        log("CPU baseline: whole steps of the stack (24 calls) on host cores")
+        result["cpu_baseline"] = cpu_mixed_baseline(cache, qs, ks, vs, windows, W)
+    return result
 
 
-def cpu_mixed_baseline(cache, q, k, v, windows, budget_s=15.0):
-    """The restated reference fallback (append + masked SDPA with GQA, torch CPU) for one call of
-    each kind the stack makes -- window 1024 and global, B=16 rows at position 4096 -- and a step
-    priced as the stack's mix of them (18 windowed calls, 6 global)."""
+def cpu_mixed_baseline(cache, qs, ks, vs, windows, first, budget_s=12.0):
+    """The restated reference fallback (append + masked SDPA with GQA, torch CPU) on whole steps
+    of the stack: the 24 calls of a step in order, each on its layer's slot and window, with the
+    same new tokens the GPU steps append, then the positions advance; median over a bounded run
+    of consecutive steps from position 4096 + `first`."""
     import torch
     from oracle import sdpa_fallback
 
     cores = host_cores()
     torch.set_num_threads(cores)
-    kc, vc = cache.k_cache[0, :, :MX_P + 1].cpu(), cache.v_cache[0, :, :MX_P + 1].cpu()
-    qc, kn, vn = q.cpu(), k.cpu(), v.cpu()
-    pos = torch.full((MX_B,), MX_P, dtype=torch.int32)
-    per = {}
+    T = MX_P + first + qs.shape[0] + 1
+    kc, vc = cache.k_cache[:, :, :T].cpu(), cache.v_cache[:, :, :T].cpu()
+    qc, kn, vn = qs.cpu(), ks.cpu(), vs.cpu()
+
+    def step(s, p):
+        pos = torch.full((MX_B,), p, dtype=torch.int32)
+        for i in range(MX_LAYERS):
+            slot = i // 2
+            sdpa_fallback.flash_attn_with_kvcache(qc[s, i], kc[slot], vc[slot], kn[s, slot],
+                                                  vn[s, slot], pos, (windows[i], 0))
+
+    times = []
     t_end = time.perf_counter() + budget_s
-    for w in (MX_WIN, -1):
-        times = []
-        sdpa_fallback.flash_attn_with_kvcache(qc, kc, vc, kn, vn, pos, (w, 0))  # warm-up
-        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
-            t0 = time.perf_counter()
-            sdpa_fallback.flash_attn_with_kvcache(qc, kc, vc, kn, vn, pos, (w, 0))
-            times.append(time.perf_counter() - t0)
-        per[w] = (statistics.median(times), len(times))
-    step = sum(per[w][0] for w in windows)
-    return {"value": round(MX_B / step, 1), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"one window-{MX_WIN} call (median of {per[MX_WIN][1]}) and one global call "
-                      f"(median of {per[-1][1]}) at B={MX_B}, position {MX_P}; step = "
-                      f"{sum(w >= 0 for w in windows)} windowed + {sum(w < 0 for w in windows)} "
-                      f"global calls; torch CPU SDPA restatement of the reference fallback"}
+    step(first, MX_P + first)  # warm-up
+    s = first
+    while s + 1 < qs.shape[0] and (len(times) < 3 or (time.perf_counter() < t_end and
+                                                       len(times) < 20)):
+        s += 1
+        t0 = time.perf_counter()
+        step(s, MX_P + s)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": round(MX_B / med, 1), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"whole steps (24 calls: {sum(w >= 0 for w in windows)} window-{MX_WIN}, "
+                      f"{sum(w < 0 for w in windows)} global, KV sharing) at B={MX_B}, positions "
+                      f"{MX_P + first + 1}+, median of {len(times)}; torch CPU SDPA restatement "
+                      f"of the reference fallback"}
 
 
 SM_LAYERS, SM_D, SM_H, SM_HKV, SM_HID, SM_V = 32, 4096, 32, 8, 14336, 32768
@@ -682,7 +697,8 @@ def cpu_sample_baseline(budget_s=20.0):
         t_head, n_head = timed(lambda: model.unembedding(x), until=t_end)
     t_layer = max(t_step - t_head, 0.0)
     step_32 = SM_LAYERS * t_layer + t_head
-    return {"value": round(SM_ROWS / step_32, 2), "unit": "tok/s", "cores": cores, "kind": "port",
+    return {"value": round(SM_ROWS / step_32, 2), "unit": "tok/s", "cores": cores,
+            "kind": "extrapolated",
             "sample": f"one decode step of a 1-layer copy of the model (fp32, oracle operator: the "
                       f"restated reference fallback), 64 rows at position {SM_PROMPT}, median of "
                       f"{n_step}; lm_head alone median of {n_head}; step = {SM_LAYERS} x "
@@ -798,7 +814,33 @@ def bench_sample(args):
     if not args.no_cpu_baseline:
         log("CPU baseline: one decode step of a 1-layer copy of the model on host cores")
         result["cpu_baseline"] = cpu_sample_baseline()
-    print(json.dumps(result), flush=True)
+    return result
+
+
+# The other workloads the default run measures beside the headline: (passes or steps timed,
+# untimed warm-up) each, fixed so that the run's length does not depend on --steps.
+SUBSYSTEM_STEPS = {"prefill": (3, 1), "mixed": (64, 8), "replicate": (10, 2)}
+SUBSYSTEM_KEEP = ("metric", "value", "unit", "ms_per_step", "steps", "warmup", "config",
+                  "roofline", "append", "cpu_baseline")
+
+
+def subsystems(args):
+    """The chunked prefill (attention MFMA utilisation and append GB/s), the mixed-window stack's
+    decode step and the replication of a prompt cache, each as its own object with its roofline
+    and a CPU baseline timed on the same work."""
+    import torch
+    out = {}
+    for name, fn in (("prefill", bench_prefill), ("mixed", bench_mixed),
+                     ("replicate", bench_replicate)):
+        steps, warmup = SUBSYSTEM_STEPS[name]
+        sub = argparse.Namespace(**{**vars(args), "steps": steps, "warmup": warmup,
+                                    "workload": name})
+        log(f"subsystem {name}: {steps} timed after {warmup} warm-up")
+        r = fn(sub)
+        out[name] = {k: r[k] for k in SUBSYSTEM_KEEP if k in r}
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(kc, vc, q, k, v, seqlens, budget_s=12.0):
@@ -836,17 +878,10 @@ def main():
     if args.calibrate_copy:
         calibrate_copy()
         return
-    if args.workload == "prefill":
-        bench_prefill(args)
-        return
-    if args.workload == "replicate":
-        bench_replicate(args)
-        return
-    if args.workload == "mixed":
-        bench_mixed(args)
-        return
-    if args.workload == "sample":
-        bench_sample(args)
+    workloads = {"prefill": bench_prefill, "replicate": bench_replicate, "mixed": bench_mixed,
+                 "sample": bench_sample}
+    if args.workload in workloads:
+        print(json.dumps(workloads[args.workload](args)), flush=True)
         return
 
     import torch
@@ -1018,6 +1053,9 @@ def main():
             "positions": "the drawn lengths (seed 0), the same for every launch",
         },
     }
+
+    if not args.decode_only:
+        result["subsystems"] = subsystems(args)
 
     if not args.no_cpu_baseline:
         log("CPU baseline: reference fallback (append + masked SDPA) on host cores")

@@ -185,6 +185,31 @@ int mcamd_prefill_attention(const void *q, const void *k_cache, const void *v_ca
                             int dtype, void *stream);
 
 /*
+ * Varlen chunked prefill: n_seqs sequences of different lengths, each appended and attended in
+ * its own cache row, with no padding. Sequence b is tokens [cu_seqlens[b], cu_seqlens[b + 1]) of
+ * the packed q (total, H, D), k and v (total, H_kv, D) and out (total, H, D), cu_seqlens being
+ * n_seqs + 1 ascending int32 offsets on the device (cu_seqlens[0] = 0); max_seqlen (>= 1) is the
+ * longest sequence's length, which sizes the grids. Sequence b uses cache row rows[b] (rows: n_seqs
+ * distinct int32 row indices on the device, or NULL for row b; not checked on the host); its query
+ * t sits at position cache_seqlens[rows[b]] + t, with the same key visibility as
+ * mcamd_flash_attn_with_kvcache. k and v (both, or neither) are appended bit-exactly at those
+ * positions first. With advance != 0, cache_seqlens[rows[b]] then grows by the sequence's length.
+ * A sequence whose positions fall outside [0, t_max) gets NaN output, and its append drops the
+ * positions past the cache (as mcamd_kv_append does).
+ * Replaces the reference's multi-prompt prefill -- each prompt prefilled alone into a batch-1
+ * cache, then copied into its row (modelcore/generate.py:67-80 -> KVCache.prefill_row,
+ * modelcore/cache.py:92-119) -- with one batched call per layer that writes every prompt's K/V in
+ * place; attention per sequence as modelcore/kernels/flash_attn.py:226-244, 362-364.
+ */
+int mcamd_flash_attn_varlen_with_kvcache(const void *q, const void *k, const void *v,
+                                         void *k_cache, void *v_cache, int32_t *cache_seqlens,
+                                         const int32_t *rows, const int32_t *cu_seqlens, void *out,
+                                         int64_t n_seqs, int64_t max_seqlen, int64_t n_head,
+                                         int64_t n_kv_head, int64_t head_dim, int64_t t_max,
+                                         int64_t cache_batch_stride, int64_t window, int causal,
+                                         int dtype, int advance, void *stream);
+
+/*
  * Next-token sampling on the device, one token per row of `logits` ((batch, vocab) fp32, rows
  * `row_stride` elements apart; 0 = every row reads the same logits): temperature 0 takes the
  * argmax (lowest index on ties); otherwise the Gumbel-max draw from softmax(logits / temperature)

@@ -22,7 +22,7 @@ LIB_PATH = Path(os.environ.get("MODELCORE_AMD_LIB",
 F32, BF16 = 0, 1
 ACT_SILU = 0  # mcamd_linear_bf16_gated activations
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH = 0, -1, -2, -3, -4
-ABI_VERSION = 7
+ABI_VERSION = 8
 NOALLOC_SCRATCH_BYTES = 32 << 20  # MCAMD_NOALLOC_SCRATCH_BYTES
 
 _i64 = ctypes.c_int64
@@ -48,6 +48,9 @@ SIGNATURES = {
     "mcamd_flash_attn_with_kvcache_noalloc": (_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
                                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                                      _i64, _int, _int, _ptr]),
+    "mcamd_flash_attn_varlen_with_kvcache": (_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
+                                                    _ptr, _ptr, _i64, _i64, _i64, _i64, _i64,
+                                                    _i64, _i64, _i64, _int, _int, _int, _ptr]),
     "mcamd_decode_attention": (_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64,
                                       _i64, _i64, _int, _ptr, _size, _ptr]),
     "mcamd_prefill_attention": (_int, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64,

@@ -149,6 +149,25 @@ class KVCache:
         self._pos_uniform = per_row[0] if len(set(per_row)) == 1 else None
         self.shared_prefix = lengths[0] if len(lengths) == 1 else 0  # one prompt: all rows alike
 
+    def fill_sample_rows(self, lengths, num_samples):
+        """After a packed prefill wrote prompt p into row p * num_samples (PackedPrefill), copy it
+        into that prompt's other sample rows [p * num_samples + 1, (p + 1) * num_samples) and set
+        every row's position to its prompt's length -- what the reference's prefill_row does per
+        prompt and sample (modelcore/cache.py:92-119), without its host reads: the lengths are
+        given. One prompt leaves every row alike (shared_prefix)."""
+        lengths = [int(n) for n in lengths]
+        assert self.batch_size == len(lengths) * num_samples, \
+            f"batch_size {self.batch_size} != {len(lengths)} prompts x {num_samples} samples"
+        for p, n in enumerate(lengths):
+            assert 0 < n <= self.max_seq_len, f"prompt of {n} tokens exceeds cache length {self.max_seq_len}"
+            if num_samples > 1:
+                self._replicate_from(self, p * num_samples + 1, num_samples - 1, n,
+                                     src_row=p * num_samples)
+        per_row = [n for n in lengths for _ in range(num_samples)]
+        self.cache_seqlens.copy_(torch.tensor(per_row, dtype=torch.int32))
+        self._pos_uniform = per_row[0] if len(set(per_row)) == 1 else None
+        self.shared_prefix = lengths[0] if len(lengths) == 1 else 0
+
     def prefill_row(self, row, other):
         """Copy a batch=1 prefilled cache into row `row` only (modelcore/cache.py:92-119); rows
         filled this way end at different positions (right-ragged)."""
@@ -169,3 +188,65 @@ class KVCache:
         # Uniform again only when every row sits at the same position (e.g. equal prompts).
         positions = set(self.cache_seqlens.tolist())
         self._pos_uniform = positions.pop() if len(positions) == 1 else None
+
+
+class PackedPrefill:
+    """Several prompts prefilled together into chosen rows of a KVCache, their tokens packed one
+    after another along a single sequence axis: ``model(idx, kv_cache=PackedPrefill(...))`` with
+    idx (1, total) runs every projection on the real tokens only (no padding), and each attention
+    layer appends prompt p's K/V at positions [0, lengths[p]) of row rows[p] and attends there
+    (``flash_attn_varlen_with_kvcache``), in place -- no transient cache, no second write. The
+    reference prefills each prompt alone into a batch-1 cache and copies it into its row
+    (modelcore/generate.py:67-80 -> KVCache.prefill_row, modelcore/cache.py:92-119).
+
+    The rows must be empty (the reference's prefill_row asserts that too); on a cache whose host
+    mirror says every row is at 0 this costs no host read. After the forward, each row sits at its
+    own prompt's length (``advance``)."""
+
+    shared_prefix = 0
+
+    def __init__(self, cache, rows, lengths):
+        rows, lengths = [int(r) for r in rows], [int(n) for n in lengths]
+        assert rows and len(rows) == len(lengths), "one cache row per prompt"
+        assert len(set(rows)) == len(rows), "rows must be distinct"
+        assert all(0 <= r < cache.batch_size for r in rows), \
+            f"rows {rows} out of range for batch_size {cache.batch_size}"
+        assert min(lengths) > 0, "empty prompt"
+        longest = max(lengths)
+        assert longest <= cache.max_seq_len, \
+            f"prompt of {longest} tokens exceeds cache length {cache.max_seq_len}"
+        if cache.uniform_pos() != 0:
+            busy = cache.cache_seqlens[rows].tolist()
+            assert not any(busy), "Cannot prefill a non-empty KV cache row"
+        dev = cache.cache_seqlens.device
+        self.cache = cache
+        self.row_list, self.lengths = rows, lengths
+        cu = [0]
+        for n in lengths:
+            cu.append(cu[-1] + n)
+        self.total, self.max_seqlen = cu[-1], longest
+        self.rows = torch.tensor(rows, dtype=torch.int32, device=dev)
+        self.cu_seqlens = torch.tensor(cu, dtype=torch.int32, device=dev)
+        # Each token's position (its index within its prompt), for RoPE.
+        self.positions = torch.cat([torch.arange(n) for n in lengths]).to(dev)
+        # Index of each prompt's last token in the packed sequence.
+        self.last = torch.tensor(cu[1:], device=dev) - 1
+
+    @property
+    def cache_seqlens(self):
+        return self.cache.cache_seqlens
+
+    def get_slot_cache(self, slot):
+        return self.cache.get_slot_cache(slot)
+
+    def advance(self, num_tokens):
+        """Each row moves on by its own prompt's length (one device add, no host read)."""
+        assert num_tokens == self.total, "a packed forward covers every prompt's tokens"
+        c = self.cache
+        c.cache_seqlens.index_add_(0, self.rows.long(),
+                                   torch.tensor(self.lengths, dtype=torch.int32,
+                                                device=c.cache_seqlens.device))
+        every = sorted(self.row_list) == list(range(c.batch_size))
+        c._pos_uniform = self.lengths[0] if (c._pos_uniform == 0 and every and
+                                             len(set(self.lengths)) == 1) else None
+        c.shared_prefix = 0

@@ -47,7 +47,7 @@ int check_attn_shapes(const AttnArgs &a, bool need_workspace) {
 
 using namespace mcamd;
 
-extern "C" int mcamd_abi_version(void) { return 7; }
+extern "C" int mcamd_abi_version(void) { return 8; }
 
 extern "C" const char *mcamd_last_error(void) { return g_last_error.c_str(); }
 
@@ -138,6 +138,44 @@ int kvcache_operator(const void *q, const void *k, const void *v, void *k_cache,
 }
 
 }  // namespace
+
+extern "C" int mcamd_flash_attn_varlen_with_kvcache(
+    const void *q, const void *k, const void *v, void *k_cache, void *v_cache,
+    int32_t *cache_seqlens, const int32_t *rows, const int32_t *cu_seqlens, void *out,
+    int64_t n_seqs, int64_t max_seqlen, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
+    int64_t t_max, int64_t cache_batch_stride, int64_t window, int causal, int dtype, int advance,
+    void *stream) {
+  (void)causal;
+  if ((k == nullptr) != (v == nullptr))
+    return fail(MCAMD_EINVAL, "flash_attn_varlen_with_kvcache: pass both k and v, or neither");
+  if (n_seqs > 0 && (!cu_seqlens || max_seqlen < 1))
+    return fail(MCAMD_EINVAL,
+                "flash_attn_varlen_with_kvcache: cu_seqlens and max_seqlen >= 1 are required");
+  AttnArgs a{q,      k,          v,      k_cache,   v_cache,  cache_seqlens,      out,
+             n_seqs, max_seqlen, n_head, n_kv_head, head_dim, t_max, cache_batch_stride,
+             window, dtype,      nullptr, 0,        as_stream(stream)};
+  a.rows = rows;
+  a.cu = cu_seqlens;
+  int st = check_attn_shapes(a, false);
+  if (st != MCAMD_OK) return st;
+  if (n_seqs == 0) {
+    clear_error();
+    return MCAMD_OK;
+  }
+  if (k) {
+    AppendArgs ap{k,         v,        k_cache, v_cache, cache_seqlens,      n_seqs, max_seqlen,
+                  n_kv_head, head_dim, t_max,   cache_batch_stride, dtype,   as_stream(stream)};
+    ap.rows = rows;
+    ap.cu = cu_seqlens;
+    st = launch_append(ap);
+    if (st != MCAMD_OK) return st;
+  }
+  a.k_new = a.v_new = nullptr;
+  st = launch_prefill(a);
+  if (st != MCAMD_OK) return st;
+  if (!advance) return MCAMD_OK;
+  return launch_advance_varlen(cache_seqlens, rows, cu_seqlens, n_seqs, as_stream(stream));
+}
 
 extern "C" int mcamd_flash_attn_with_kvcache(const void *q, const void *k, const void *v,
                                              void *k_cache, void *v_cache,

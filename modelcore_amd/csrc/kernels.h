@@ -13,11 +13,19 @@ struct AppendArgs {
   int64_t batch, t_new, n_kv_head, head_dim, t_max, cache_batch_stride;
   int dtype;
   hipStream_t stream;
+  // Varlen form (both optional): sequence b writes cache row rows[b] (b when null), and its new
+  // tokens are [cu[b], cu[b + 1]) of k/v (t_new each, packed by sequence, when null); with cu,
+  // t_new is the longest sequence's length.
+  const int32_t *rows = nullptr;
+  const int32_t *cu = nullptr;
 };
 int launch_append(const AppendArgs &a);
 
 // seqlens[b] += advance for b < batch, one small kernel on `stream`.
 int launch_advance(int32_t *seqlens, int64_t batch, int advance, hipStream_t stream);
+// Varlen form: seqlens[rows[b]] += cu[b + 1] - cu[b] for b < n_seqs (rows null: row b).
+int launch_advance_varlen(int32_t *seqlens, const int32_t *rows, const int32_t *cu,
+                          int64_t n_seqs, hipStream_t stream);
 
 struct AttnArgs {
   const void *q;
@@ -40,6 +48,11 @@ struct AttnArgs {
   // prompt): the bf16 / head_dim 128 decode reads them from row 0 for every row, so the rows'
   // repeated reads of those lines hit the caches. The other paths read each row's own copy.
   int64_t shared_prefix = 0;
+  // Varlen prefill (launch_prefill only; both optional): sequence b uses cache row rows[b] (b when
+  // null; cache_seqlens is indexed by the row) and its queries are tokens [cu[b], cu[b + 1]) of q
+  // and out (t_new each when null; with cu, t_new is the longest sequence's length).
+  const int32_t *rows = nullptr;
+  const int32_t *cu = nullptr;
 };
 int launch_decode(const AttnArgs &a);
 int launch_prefill(const AttnArgs &a);

@@ -26,21 +26,25 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 constexpr int kUnroll = 2;
 
+// Sequence b = b_first + blockIdx.z goes to cache row rows[b] (b when rows is null); its new
+// tokens are t_new consecutive tokens from token b * t_new of k/v, or, with cu (the varlen form:
+// sequences of different lengths packed one after another), tokens [cu[b], cu[b + 1]).
 template <class U, bool POW2>
-__global__ __launch_bounds__(kThreads) void kv_append_kernel(const U *__restrict__ k,
-                                                             const U *__restrict__ v,
-                                                             U *__restrict__ k_cache,
-                                                             U *__restrict__ v_cache,
-                                                             const int32_t *__restrict__ seqlens,
-                                                             int t_new, int units_per_row,
-                                                             int upr_shift, int64_t t_max,
-                                                             int64_t cache_b_units) {
-  const int b = blockIdx.z;
-  const U *src = (blockIdx.y == 0 ? k : v) + int64_t(b) * t_new * units_per_row;
-  U *dst = (blockIdx.y == 0 ? k_cache : v_cache) + int64_t(b) * cache_b_units;
-  const int64_t s0 = seqlens[b];
-  const int row_units = t_new * units_per_row;  // this row's units (fits 32 bits: checked)
+__global__ __launch_bounds__(kThreads) void kv_append_kernel(
+    const U *__restrict__ k, const U *__restrict__ v, U *__restrict__ k_cache,
+    U *__restrict__ v_cache, const int32_t *__restrict__ seqlens, const int32_t *__restrict__ rows,
+    const int32_t *__restrict__ cu, int b_first, int t_new, int units_per_row, int upr_shift,
+    int64_t t_max, int64_t cache_b_units) {
+  const int b = b_first + int(blockIdx.z);
+  const int row = rows ? rows[b] : b;
+  const int64_t tok0 = cu ? int64_t(cu[b]) : int64_t(b) * t_new;
+  const int t_b = cu ? cu[b + 1] - cu[b] : t_new;
+  const U *src = (blockIdx.y == 0 ? k : v) + tok0 * units_per_row;
+  U *dst = (blockIdx.y == 0 ? k_cache : v_cache) + int64_t(row) * cache_b_units;
+  const int64_t s0 = seqlens[row];
+  const int row_units = t_b * units_per_row;  // this row's units (fits 32 bits: checked)
   const int base = blockIdx.x * (kThreads * kUnroll);
+  if (base >= row_units) return;  // varlen: a shorter sequence than the grid's longest
   const int first = base + threadIdx.x;
   const int last = std::min(base + kThreads * kUnroll, row_units) - 1;  // uniform
   const int t_first = POW2 ? base >> upr_shift : base / units_per_row;
@@ -85,6 +89,7 @@ int run(const AppendArgs &a, int64_t row_bytes) {
     return fail(MCAMD_EUNSUPPORTED, "kv_append: too many units in one row's new tokens for 32-bit "
                                     "indices");
   const int64_t per_block = int64_t(kThreads) * kUnroll;
+  // Varlen: t_new is the longest sequence's token count (sizes the grid).
   const unsigned blocks = unsigned((a.t_new * upr + per_block - 1) / per_block);
   int shift = 0;
   while ((int64_t(1) << shift) < upr) ++shift;
@@ -92,15 +97,12 @@ int run(const AppendArgs &a, int64_t row_bytes) {
   // Rows go in the grid's z dimension, at most 65535 per launch.
   constexpr int64_t kRowsPerLaunch = 65535;
   for (int64_t b0 = 0; b0 < a.batch; b0 += kRowsPerLaunch) {
-    const int64_t rows = std::min(kRowsPerLaunch, a.batch - b0);
-    const int64_t src_off = b0 * a.t_new * upr;
-    const dim3 grid(blocks, 2, unsigned(rows));
+    const int64_t n = std::min(kRowsPerLaunch, a.batch - b0);
+    const dim3 grid(blocks, 2, unsigned(n));
     auto go = [&](auto kernel) {
-      hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, a.stream,
-                         static_cast<const U *>(a.k) + src_off,
-                         static_cast<const U *>(a.v) + src_off,
-                         static_cast<U *>(a.k_cache) + b0 * cb_units,
-                         static_cast<U *>(a.v_cache) + b0 * cb_units, a.seqlens + b0,
+      hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, a.stream, static_cast<const U *>(a.k),
+                         static_cast<const U *>(a.v), static_cast<U *>(a.k_cache),
+                         static_cast<U *>(a.v_cache), a.seqlens, a.rows, a.cu, int(b0),
                          int(a.t_new), int(upr), shift, a.t_max, cb_units);
     };
     if (pow2)
@@ -117,7 +119,27 @@ __global__ __launch_bounds__(256) void advance_kernel(int32_t *seqlens, int batc
   for (int b = blockIdx.x * 256 + threadIdx.x; b < batch; b += gridDim.x * 256) seqlens[b] += by;
 }
 
+__global__ __launch_bounds__(256) void advance_varlen_kernel(int32_t *seqlens,
+                                                             const int32_t *rows,
+                                                             const int32_t *cu, int n) {
+  for (int b = blockIdx.x * 256 + threadIdx.x; b < n; b += gridDim.x * 256)
+    seqlens[rows ? rows[b] : b] += cu[b + 1] - cu[b];
+}
+
 }  // namespace
+
+int launch_advance_varlen(int32_t *seqlens, const int32_t *rows, const int32_t *cu,
+                          int64_t n_seqs, hipStream_t stream) {
+  if (n_seqs <= 0) {
+    clear_error();
+    return MCAMD_OK;
+  }
+  if (!seqlens || !cu) return fail(MCAMD_EINVAL, "advance: null cache_seqlens or cu_seqlens");
+  const int blocks = int(std::min<int64_t>((n_seqs + 255) / 256, 256));
+  hipLaunchKernelGGL(advance_varlen_kernel, dim3(blocks), dim3(256), 0, stream, seqlens, rows,
+                     cu, int(n_seqs));
+  return launch_status("advance_varlen");
+}
 
 int launch_advance(int32_t *seqlens, int64_t batch, int advance, hipStream_t stream) {
   if (batch <= 0 || advance == 0) {

@@ -28,6 +28,7 @@ constexpr int KT = 32;
 struct PrefillParams {
   const void *q, *k_cache, *v_cache;
   const int32_t *seqlens;
+  const int32_t *rows, *cu;  // varlen (optional): cache row and token range per sequence
   void *out;
   int T_new, H, H_kv, G, QT, T_max, window, D;
   int64_t cache_b;
@@ -44,22 +45,26 @@ __global__ __launch_bounds__(kThreads) void prefill_generic_kernel(PrefillParams
 
   const int qt0 = blockIdx.x * P.QT;
   const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
+  const int b = blockIdx.z;  // sequence; varlen: tokens [cu[b], cu[b + 1]) in cache row rows[b]
+  const int crow = P.rows ? P.rows[b] : b;
+  const int64_t tok0 = P.cu ? int64_t(P.cu[b]) : int64_t(b) * P.T_new;
+  const int T_b = P.cu ? P.cu[b + 1] - P.cu[b] : P.T_new;
+  if (qt0 >= T_b) return;  // a query tile past a shorter sequence's end (whole workgroup)
   const int tid = threadIdx.x;
   const int row = tid >> 2;
   const int j = tid & 3;
   const int tq = qt0 + row / P.G;
   const int g = row - (row / P.G) * P.G;
   const int h = kvh * P.G + g;
-  const bool active = (row < P.QT * P.G) && (tq < P.T_new);
+  const bool active = (row < P.QT * P.G) && (tq < T_b);
 
-  const int pos = P.seqlens[b];
-  const int q_last = min(qt0 + P.QT, P.T_new) - 1;
-  const bool row_ok = pos >= 0 && pos + P.T_new <= P.T_max;
+  const int pos = P.seqlens[crow];
+  const int q_last = min(qt0 + P.QT, T_b) - 1;
+  const bool row_ok = pos >= 0 && pos + T_b <= P.T_max;
 
   const E *q = static_cast<const E *>(P.q);
   E *out = static_cast<E *>(P.out);
-  const int64_t out_off = ((int64_t(b) * P.T_new + tq) * P.H + h) * D;
+  const int64_t out_off = ((tok0 + tq) * P.H + h) * D;
 
   if (!row_ok) {
     if (active)
@@ -89,8 +94,8 @@ __global__ __launch_bounds__(kThreads) void prefill_generic_kernel(PrefillParams
   const int klo = P.window >= 0 ? max(0, p_first - P.window) : 0;
   const int khi = p_last;
 
-  const E *kc = static_cast<const E *>(P.k_cache) + int64_t(b) * P.cache_b + int64_t(kvh) * D;
-  const E *vc = static_cast<const E *>(P.v_cache) + int64_t(b) * P.cache_b + int64_t(kvh) * D;
+  const E *kc = static_cast<const E *>(P.k_cache) + int64_t(crow) * P.cache_b + int64_t(kvh) * D;
+  const E *vc = static_cast<const E *>(P.v_cache) + int64_t(crow) * P.cache_b + int64_t(kvh) * D;
   const int64_t tok_stride = int64_t(P.H_kv) * D;
 
   for (int kt0 = klo; kt0 <= khi; kt0 += KT) {
@@ -185,6 +190,8 @@ int launch_prefill_generic(const AttnArgs &a) {
   P.k_cache = a.k_cache;
   P.v_cache = a.v_cache;
   P.seqlens = a.seqlens;
+  P.rows = a.rows;
+  P.cu = a.cu;
   P.out = a.out;
   P.T_new = int(a.t_new);
   P.H = int(a.n_head);

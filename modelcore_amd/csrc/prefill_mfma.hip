@@ -74,6 +74,7 @@ typedef __bf16 lds_bf16x4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
 struct MfmaParams {
   const uint16_t *q, *k_cache, *v_cache;
   const int32_t *seqlens;
+  const int32_t *rows, *cu;  // varlen prefill (optional): cache row and token range per sequence
   uint16_t *out;
   int T_new, H, H_kv, G, QT, T_max, window, n_bh;
   int64_t cache_b;
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
   const int bh = blockIdx.x % P.n_bh;
   const int qt = PREFIX ? (blockIdx.x / P.n_bh) % P.n_qt : blockIdx.x / P.n_bh;
   const int split = PREFIX ? blockIdx.x / (P.n_bh * P.n_qt) : 0;
-  const int b = bh / P.H_kv;
+  const int b = bh / P.H_kv;  // sequence (a cache row, or one prompt of a varlen batch)
   const int kvh = bh - b * P.H_kv;
   const int q0 = qt * P.QT;
   const int tid = threadIdx.x;
@@ -152,16 +153,22 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
   const int h = lane >> 5;    // lane half
   const int col = lane & 31;  // this lane's pair within the wave's 32
 
-  const int s0 = PREFIX ? 0 : P.seqlens[b];
-  const int q_end = min(q0 + P.QT, P.T_new);  // positions [q0, q_end) of the chunk
-  const bool row_ok = PREFIX || (s0 >= 0 && int64_t(s0) + P.T_new <= P.T_max);
+  // Varlen: sequence b's queries are tokens [cu[b], cu[b + 1]) of q/out, its keys cache row
+  // rows[b]; a query tile past the sequence's end has nothing to do (a whole workgroup).
+  const int row = (PREFIX || !P.rows) ? b : P.rows[b];
+  const int64_t tok0 = P.cu ? int64_t(P.cu[b]) : int64_t(b) * P.T_new;
+  const int T_b = P.cu ? P.cu[b + 1] - P.cu[b] : P.T_new;
+  if (q0 >= T_b) return;
+  const int s0 = PREFIX ? 0 : P.seqlens[row];
+  const int q_end = min(q0 + P.QT, T_b);  // positions [q0, q_end) of the chunk
+  const bool row_ok = PREFIX || (s0 >= 0 && int64_t(s0) + T_b <= P.T_max);
 
   const int pr = wave * 32 + col;
   const bool live = pr < P.QT * P.G && q0 + pr / P.G < q_end;
   const int pos = live ? q0 + pr / P.G : q0;  // dead pairs compute on a live position
   const int head = live ? pr - (pr / P.G) * P.G : 0;
   uint16_t *out =
-      PREFIX ? nullptr : P.out + ((int64_t(b) * P.T_new + pos) * P.H + int64_t(kvh) * P.G + head) * D;
+      PREFIX ? nullptr : P.out + ((tok0 + pos) * P.H + int64_t(kvh) * P.G + head) * D;
   if (!row_ok) {
     if (live)
       for (int d = h * 64; d < h * 64 + 64; ++d) out[d] = 0x7fc0;
@@ -171,8 +178,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
   // Q^T fragments: B[k = dim][n = pair], lane holds pair `col`, dims 16 kd + 8 h .. + 7.
   bf16x8 qf[8];
   {
-    const uint16_t *qp =
-        P.q + ((int64_t(b) * P.T_new + pos) * P.H + int64_t(kvh) * P.G + head) * D + 8 * h;
+    const uint16_t *qp = P.q + ((tok0 + pos) * P.H + int64_t(kvh) * P.G + head) * D + 8 * h;
 #pragma unroll
     for (int kd = 0; kd < 8; ++kd)
       qf[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(qp + 16 * kd));
@@ -187,8 +193,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
   const int hi = p_last;
 
   const int64_t tok = int64_t(P.H_kv) * D;
-  const uint16_t *kbase = P.k_cache + int64_t(b) * P.cache_b + int64_t(kvh) * D;
-  const uint16_t *vbase = P.v_cache + int64_t(b) * P.cache_b + int64_t(kvh) * D;
+  const uint16_t *kbase = P.k_cache + int64_t(row) * P.cache_b + int64_t(kvh) * D;
+  const uint16_t *vbase = P.v_cache + int64_t(row) * P.cache_b + int64_t(kvh) * D;
 
   // A tile takes 32 DMA instructions of 1 KiB (16 K fragments, 16 blocks of 4 V rows); wave w
   // issues K fragments 2w, 2w + 1 and V blocks 2w, 2w + 1. Keys past `hi` re-read key `hi` (they
@@ -508,6 +514,8 @@ int launch_prefill_mfma(const AttnArgs &a) {
   P.k_cache = static_cast<const uint16_t *>(a.k_cache);
   P.v_cache = static_cast<const uint16_t *>(a.v_cache);
   P.seqlens = a.seqlens;
+  P.rows = a.rows;
+  P.cu = a.cu;
   P.out = static_cast<uint16_t *>(a.out);
   P.T_new = int(a.t_new);
   P.H = int(a.n_head);
@@ -533,6 +541,7 @@ int launch_prefix_partials(const PrefixArgs &a) {
   P.k_cache = static_cast<const uint16_t *>(a.k_cache);
   P.v_cache = static_cast<const uint16_t *>(a.v_cache);
   P.seqlens = nullptr;
+  P.rows = P.cu = nullptr;
   P.out = nullptr;
   P.T_new = int(a.rows);
   P.H = int(a.n_head);

@@ -3,14 +3,17 @@
 
 ``Decoder`` prefills a prompt at batch 1, replicates its cache into ``num_samples`` rows with the
 HIP replication kernel (``KVCache.prefill``), then steps every row one position per call. Several
-prompts are prefilled together, right-padded to the longest, and each is copied into its own
-right-ragged rows (``KVCache.prefill_rows``); row ``p * num_samples + s`` is sample ``s`` of
-prompt ``p``.
+prompts are prefilled together as one packed sequence (``PackedPrefill``: no padding), each
+written straight into its first sample row and copied into the others
+(``KVCache.fill_sample_rows``), the rows right-ragged; row ``p * num_samples + s`` is sample ``s``
+of prompt ``p``.
 """
 from __future__ import annotations
 
 import torch
 import torch.nn.functional as F
+
+from modelcore_amd.cache import PackedPrefill
 
 
 @torch.inference_mode()
@@ -47,26 +50,24 @@ class Decoder:
                                                  device=device)
             self.kv_cache.prefill(prefill)
             return
-        # Several prompts: one batched prefill of the prompts right-padded to the longest (causal
-        # attention keeps every prompt's positions blind to its padding), then each prompt's row
-        # copied into its samples' rows at its own length -- in place of the reference's prefill
-        # and prefill_row per prompt (modelcore/generate.py:67-80), with no host reads.
+        # Several prompts: one packed forward of all their tokens (no padding) that writes prompt
+        # p's K/V straight into row p * num_samples of the decode cache (PackedPrefill, the varlen
+        # operator), then copies of that row into the prompt's other sample rows -- in place of
+        # the reference's per-prompt batch-1 prefill and prefill_row copies
+        # (modelcore/generate.py:67-80), with no transient cache and no host reads.
         prompts = [list(p) for p in tokens]
         lengths = [len(p) for p in prompts]
         assert min(lengths) > 0, "empty prompt"
         longest = max(lengths)
         length = longest + max_tokens if max_tokens is not None else model.config.sequence_len
-        prefill = manager.new_kv_cache(model, batch_size=len(prompts), seq_len=longest,
-                                       device=device)
-        ids = torch.zeros(len(prompts), longest, dtype=torch.long)
-        for p, prompt in enumerate(prompts):
-            ids[p, :len(prompt)] = torch.tensor(prompt, dtype=torch.long)
-        last = torch.tensor(lengths) - 1
-        logits = model.last_logits(ids.to(device), prefill, last)
         self.kv_cache = manager.new_kv_cache(model, batch_size=len(prompts) * num_samples,
                                              seq_len=length, device=device)
-        self.kv_cache.prefill_rows(prefill, lengths, num_samples)
-        del prefill
+        packed = PackedPrefill(self.kv_cache, [p * num_samples for p in range(len(prompts))],
+                               lengths)
+        ids = torch.tensor([t for prompt in prompts for t in prompt], dtype=torch.long,
+                           device=device).unsqueeze(0)
+        logits = model.last_logits(ids, packed, None)
+        self.kv_cache.fill_sample_rows(lengths, num_samples)
         self._logits = logits.repeat_interleave(num_samples, dim=0)
 
     @property

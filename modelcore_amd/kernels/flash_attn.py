@@ -218,6 +218,88 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
     return out
 
 
+def flash_attn_varlen_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
+                                   cu_seqlens=None, max_seqlen=None, rows=None, causal=False,
+                                   window_size=(-1, -1), *, advance=False):
+    """Varlen cached attention: several sequences of different lengths packed along one token
+    axis, each appended and attended in its own cache row, with no padding. Extension with no
+    single counterpart in the reference: it replaces the multi-prompt prefill's one prefill per
+    prompt into a batch-1 cache followed by a copy into its row (modelcore/generate.py:67-80 ->
+    KVCache.prefill_row, modelcore/cache.py:92-119) with one call per layer that writes every
+    prompt's K/V in place.
+
+    Args:
+        q: (total, H, D) packed queries; sequence b is tokens [cu_seqlens[b], cu_seqlens[b + 1])
+        k_cache, v_cache: (B_cache, T_max, H_kv, D) caches, updated in place
+        k, v: (total, H_kv, D) new keys/values, or both None
+        cache_seqlens: (B_cache,) int32 positions; sequence b starts at cache_seqlens[rows[b]]
+        cu_seqlens: (n + 1,) int32 on the device, ascending from 0
+        max_seqlen: the longest sequence's length (host int)
+        rows: (n,) int32 distinct cache rows on the device, or None for rows 0..n-1
+        window_size: (left, right); left = -1 means unlimited
+        advance: after the call, every sequence's row moves on by its length (device side)
+
+    Returns:
+        (total, H, D) tensor in q's dtype.
+    """
+    _ext.require_rocm(q, k_cache, v_cache, k, v, cache_seqlens, cu_seqlens, rows,
+                      what="flash_attn_varlen_with_kvcache")
+    if q.dim() != 3:
+        raise ValueError(f"q must be (total, H, D); got {tuple(q.shape)}")
+    total, H, D = q.shape
+    if (k is None) != (v is None):
+        raise ValueError("pass both k and v, or neither")
+    if cu_seqlens is None or cu_seqlens.dtype != torch.int32 or cu_seqlens.dim() != 1 \
+            or cu_seqlens.numel() < 1:
+        raise ValueError("cu_seqlens must be a (n + 1,) int32 tensor")
+    n = cu_seqlens.numel() - 1
+    if rows is not None and (rows.dtype != torch.int32 or rows.shape != (n,)):
+        raise ValueError(f"rows must be ({n},) int32; got {tuple(rows.shape)} {rows.dtype}")
+    if max_seqlen is None or int(max_seqlen) < 1:
+        raise ValueError("max_seqlen (the longest sequence's length, >= 1) is required")
+    H_kv = None
+    if k is not None:
+        if k.shape != v.shape or k.dim() != 3 or k.shape[0] != total or k.shape[2] != D:
+            raise ValueError(f"k/v must be (total, H_kv, D) = ({total}, H_kv, {D}); got "
+                             f"{tuple(k.shape)} and {tuple(v.shape)}")
+        H_kv = k.shape[1]
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
+        raise ValueError(f"k_cache/v_cache must both be (B, T_max, H_kv, D); got "
+                         f"{tuple(k_cache.shape)} and {tuple(v_cache.shape)}")
+    B_cache = k_cache.shape[0]
+    T_max, H_kv = _check_cache(k_cache, v_cache, B_cache, H_kv, D)
+    dt = q.dtype
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache), ("k", k), ("v", v)):
+        if t is not None and t.dtype != dt:
+            raise TypeError(f"{name} is {t.dtype}, q is {dt}")
+    code = _ext.dtype_code(dt)
+    seqlens = _check_seqlens(cache_seqlens, B_cache, q.device)
+    if advance and seqlens.data_ptr() != cache_seqlens.data_ptr():
+        raise ValueError("advance needs cache_seqlens itself to be contiguous (it is updated in "
+                         "place)")
+    if CHECK_POSITIONS and n > 0:
+        lens = (cu_seqlens[1:] - cu_seqlens[:-1]).long()
+        base = seqlens.long()[rows.long()] if rows is not None else seqlens.long()[:n]
+        lo, hi = int(base.min()), int((base + lens).max())
+        if lo < 0 or hi > T_max:
+            raise IndexError(f"flash_attn_varlen_with_kvcache: positions [{lo}, {hi}) of the new "
+                             f"tokens fall outside the cache of {T_max} positions")
+    q = q.contiguous()
+    if k is not None:
+        k, v = k.contiguous(), v.contiguous()
+    out = torch.empty_like(q)
+    lib = _ext.lib()
+    st = lib.mcamd_flash_attn_varlen_with_kvcache(
+        q.data_ptr(), k.data_ptr() if k is not None else None,
+        v.data_ptr() if v is not None else None, k_cache.data_ptr(), v_cache.data_ptr(),
+        seqlens.data_ptr(), rows.data_ptr() if rows is not None else None,
+        cu_seqlens.contiguous().data_ptr(), out.data_ptr(), n, int(max_seqlen), H, H_kv, D, T_max,
+        k_cache.stride(0), _window(window_size), int(bool(causal)), code, int(bool(advance)),
+        _ext.stream_handle(q.device))
+    _ext.check(st, "flash_attn_varlen_with_kvcache")
+    return out
+
+
 def flash_attn_func(q, k, v, causal=False, window_size=(-1, -1), doc_args=None):
     """No-cache attention (modelcore/kernels/flash_attn.py:270-303), inference only.
 
@@ -258,6 +340,7 @@ def flash_attn_func(q, k, v, causal=False, window_size=(-1, -1), doc_args=None):
 flash_attn = SimpleNamespace(
     flash_attn_func=flash_attn_func,
     flash_attn_with_kvcache=flash_attn_with_kvcache,
+    flash_attn_varlen_with_kvcache=flash_attn_varlen_with_kvcache,
     # Keyword arguments of flash_attn_with_kvcache beyond the reference's (callers check this
     # before passing them, so that an operator without them can stand in).
     EXTENSIONS=frozenset({"advance", "shared_prefix"}),

@@ -27,7 +27,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from modelcore_amd.cache import KVCache
+from modelcore_amd.cache import KVCache, PackedPrefill
 from modelcore_amd.runtime import Runtime
 
 TYPE_KEY = "#type"
@@ -209,6 +209,12 @@ class Rotary(nn.Module):
         assert last < self.cos.size(1), \
             f"Sequence length grew beyond the rotary embeddings cache: {last + 1} > {self.cos.size(1)}"
 
+    def packed_cos_sin(self, positions):
+        """cos/sin at each token's own position, (1, N, 1, head_dim/2), for a packed forward of
+        several prompts (PackedPrefill); positions are host-known to fit the table."""
+        return (self.cos[0, :, 0].index_select(0, positions)[None, :, None, :],
+                self.sin[0, :, 0].index_select(0, positions)[None, :, None, :])
+
     def forward(self, q, k, kv_cache):
         cos, sin = self._cos_sin(q.size(1), kv_cache)
         return rotate(q, cos, sin), rotate(k, cos, sin)
@@ -339,10 +345,12 @@ class Attention(nn.Module):
         each row's position from cache_seqlens on the device (the separate ops slice the tables
         at the host-side position instead)."""
         return kv_cache is not None and self.epilogue is not None and self.fuse_epilogue \
-            and isinstance(self.norm, RMSNorm)
+            and isinstance(self.norm, RMSNorm) and not isinstance(kv_cache, PackedPrefill)
 
     def forward(self, x, kv_cache, kv_bus):
         B, T, _ = x.size()
+        if isinstance(kv_cache, PackedPrefill):
+            return self._forward_packed(x, kv_cache, kv_bus)
         fused = self.fuses_epilogue(kv_cache)
         if fused:
             part = self._qkv_partials(x)
@@ -371,6 +379,30 @@ class Attention(nn.Module):
         if "output_gate" in self.features:
             y = self.features["output_gate"](y, x)
         return self.c_proj(y.contiguous().view(B, T, -1))
+
+    def _forward_packed(self, x, packed, kv_bus):
+        """The layer over several prompts packed along one sequence (x is (1, total, n_embd)):
+        projections on the real tokens only, RoPE at each token's position within its prompt,
+        QK-norm and x1.2 as the reference's separate ops, then the varlen operator appends each
+        prompt's K/V into its own cache row and attends there."""
+        _, T, _ = x.size()
+        q, k, v = self._project(x)
+        cos, sin = self.rope.packed_cos_sin(packed.positions)
+        if self.produces_kv:
+            q, k = rotate(q, cos, sin), rotate(k, cos, sin)
+            q, k = self.norm(q) * 1.2, self.norm(k) * 1.2
+            kv_bus[self.kv_slot] = (k, v)
+        else:
+            k, v = kv_bus[self.kv_slot]
+            q = self.norm(rotate(q, cos, sin)) * 1.2
+        k_cache, v_cache = packed.get_slot_cache(self.kv_slot)
+        y = self.attention.flash_attn_varlen_with_kvcache(
+            q[0], k_cache, v_cache, k=k[0], v=v[0], cache_seqlens=packed.cache_seqlens,
+            cu_seqlens=packed.cu_seqlens, max_seqlen=packed.max_seqlen, rows=packed.rows,
+            causal=True, window_size=(self.window, 0)).unsqueeze(0)
+        if "output_gate" in self.features:
+            y = self.features["output_gate"](y, x)
+        return self.c_proj(y.contiguous().view(1, T, -1))
 
     def _extensions(self, kv_cache):
         """Operator keywords beyond the reference's, for an operator that takes them: the
@@ -765,6 +797,11 @@ class Model(nn.Module):
         (an index error past T_max), which the kernels cannot raise, so the check is made here
         -- free on a uniform cache (the host mirror), one host read on a ragged one (as the
         ragged RoPE gather makes anyway)."""
+        if isinstance(kv_cache, PackedPrefill):
+            # Empty rows and prompt lengths within the cache and the rotary table: checked when
+            # the packed batch was made, apart from the table's length.
+            assert kv_cache.max_seqlen <= kv_cache.cache.max_seq_len
+            return
         pos = kv_cache.uniform_pos()
         last = pos + T if pos is not None else int(kv_cache.cache_seqlens.max().item()) + T
         assert last <= kv_cache.max_seq_len, \
@@ -784,10 +821,22 @@ class Model(nn.Module):
     def last_logits(self, idx, kv_cache, last):
         """forward(), but the head runs only at position last[b] of row b: (B, vocab) logits.
         The head is per position, so these equal forward()[b, last[b]]; a prompt prefill needs
-        only its last position, and skips the (B, T, vocab) logits of all the others."""
+        only its last position, and skips the (B, T, vocab) logits of all the others. With a
+        PackedPrefill, idx is every prompt's tokens as one (1, total) sequence, `last` is not
+        used, and the logits are those of each prompt's last token, (prompts, vocab)."""
         self.check_cache_room(kv_cache, idx.size(1))
+        if isinstance(kv_cache, PackedPrefill):
+            assert idx.size(0) == 1 and idx.size(1) == kv_cache.total, \
+                "a packed prefill takes every prompt's tokens as one (1, total) sequence"
+            n_pos = min(b.mixer.rope.cos.size(1) for b in self.body.blocks)
+            assert kv_cache.max_seqlen <= n_pos, \
+                f"Sequence length grew beyond the rotary embeddings cache: {kv_cache.max_seqlen} > {n_pos}"
         x, h = self.body.forward_carry(self.embedding(idx), kv_cache)
         kv_cache.advance(idx.size(1))
+        if isinstance(kv_cache, PackedPrefill):  # (prompts, vocab) at each prompt's last token
+            last = kv_cache.last
+            return self.unembedding(x[0, last].unsqueeze(1),
+                                    None if h is None else h[0, last].unsqueeze(1))[:, 0]
         rows = torch.arange(idx.size(0), device=x.device)
         last = last.to(x.device)
         return self.unembedding(x[rows, last].unsqueeze(1),

@@ -8,6 +8,9 @@
   (Tq, Tk) mask for uniform chunks (:226-244), a (B, 1, T_new, Tk) mask when ragged (:246-264).
 * ``flash_attn_func`` follows the no-cache fallback (modelcore/kernels/flash_attn.py:270-303
   without FA3 or document masks): transpose to (B, H, T, D), then the same uniform helper.
+* ``flash_attn_varlen_with_kvcache`` is the varlen (packed prompts) form: the operator above run
+  once per sequence on its own cache row, as the reference prefills each prompt alone
+  (modelcore/generate.py:67-80).
 * ``replicate`` follows KVCache.prefill's broadcast copy (modelcore/cache.py:84-85).
 * ``flash_attn`` is the operator namespace of the two functions, for model code that takes one.
 """
@@ -84,8 +87,35 @@ def flash_attn_func(q, k, v, causal=True, window_size=(-1, -1), doc_args=None):
     return y.transpose(1, 2)
 
 
+def flash_attn_varlen_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
+                                   cu_seqlens=None, max_seqlen=None, rows=None, causal=True,
+                                   window_size=(-1, -1), advance=False):
+    """Several sequences packed along one token axis, each appended and attended in its own
+    cache row: sequence b is tokens [cu_seqlens[b], cu_seqlens[b + 1]) of q (total, H, D) and k/v
+    (total, H_kv, D), in row rows[b] (b when None). The reference prefills each prompt alone and
+    copies it into its row (modelcore/generate.py:67-80, modelcore/cache.py:92-119); this runs
+    the fallback above once per sequence on that row, which is the same arithmetic. With
+    `advance`, each row's position then moves on by its sequence's length."""
+    cu = [int(x) for x in cu_seqlens.tolist()]
+    n = len(cu) - 1
+    rows = list(range(n)) if rows is None else [int(r) for r in rows.tolist()]
+    outs = []
+    for b in range(n):
+        r, a, e = rows[b], cu[b], cu[b + 1]
+        kb = None if k is None else k[a:e].unsqueeze(0)
+        vb = None if v is None else v[a:e].unsqueeze(0)
+        y = flash_attn_with_kvcache(q[a:e].unsqueeze(0), k_cache[r:r + 1], v_cache[r:r + 1], kb,
+                                    vb, cache_seqlens[r:r + 1], window_size)
+        outs.append(y[0])
+    if advance:
+        for b in range(n):
+            cache_seqlens[rows[b]] += cu[b + 1] - cu[b]
+    return torch.cat(outs, 0) if outs else q.new_empty((0,) + tuple(q.shape[1:]))
+
+
 flash_attn = SimpleNamespace(flash_attn_func=flash_attn_func,
-                             flash_attn_with_kvcache=flash_attn_with_kvcache)
+                             flash_attn_with_kvcache=flash_attn_with_kvcache,
+                             flash_attn_varlen_with_kvcache=flash_attn_varlen_with_kvcache)
 
 
 def replicate(dst_k, dst_v, src_k, src_v, n_tokens):

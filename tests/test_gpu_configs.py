@@ -150,8 +150,8 @@ def _decode(mgr, model, prompts, samples, n, feed=None):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_batched_multi_prompt_decoder_matches_the_cpu_oracle(dtype, cpu_cache_copies):  # noqa: F811
     """The reference's multi-prompt flow (modelcore/generate.py:67-80 -> cache.py:92-119) is
-    one prefill and prefill_row per prompt; this build prefills the prompts together and places
-    each row at its own length. Both sides run this build's Decoder; the CPU one attends through
+    one prefill and prefill_row per prompt; this build prefills the prompts together as one
+    packed sequence that writes each prompt's K/V into its own row in place. Both sides run this build's Decoder; the CPU one attends through
     the oracle operator (whose Decoder equals per-prompt decoding, test_model_host.py). fp32:
     the greedy ids are identical; bf16: fed the CPU's greedy ids, every step's logits stay within
     bf16 tolerance."""
@@ -170,7 +170,9 @@ def test_batched_multi_prompt_decoder_matches_the_cpu_oracle(dtype, cpu_cache_co
         feed = None if dtype == torch.float32 else want_ids
         got_ids, got_logits, got_len = _decode(gpu_mgr, gpu_model, prompts, 2, 8, feed)
     assert torch.equal(got_len, want_len)
-    tol = 2e-4 if dtype == torch.float32 else 0.15
+    # bf16 against the fp32 CPU oracle: weights, activations and K/V rounded to bf16 move these
+    # logits (scale ~0.07) by up to ~2e-3, as in the single-prompt stack test
+    tol = 2e-4 if dtype == torch.float32 else 5e-3
     for i, (a, b) in enumerate(zip(got_logits, want_logits)):
         err = (a - b).abs().max().item()
         print(f"step {i}: logits max-abs {err:.2e} (scale {b.abs().max().item():.2f})", flush=True)

@@ -159,7 +159,9 @@ def test_mixed_window_kv_sharing_stack_in_bf16(cpu_cache_copies):
     for i, (a, b) in enumerate(zip(got, want)):
         err = (a - b).abs().max().item()
         print(f"call {i}: logits max-abs {err:.4f} (scale {b.abs().max().item():.3f})", flush=True)
-        assert err <= 0.15, f"call {i}: logits max-abs {err}"
+        # bf16 rounding of weights, activations and K/V against the fp32 CPU oracle: ~2e-3 on
+        # logits of scale ~0.07
+        assert err <= 5e-3, f"call {i}: logits max-abs {err}"
     assert gpu_cache.cache_seqlens.tolist() == [P + steps] * B
 
 
@@ -384,10 +386,10 @@ def test_captured_decode_step_replays_the_eager_steps(fast, top_k):
 
 
 def test_batched_multi_prompt_prefill_matches_one_prefill_per_prompt():
-    """Ragged prompts prefilled together (right-padded, then KVCache.prefill_rows) against the
-    reference's flow of one prefill and prefill_row per prompt, bf16 on the GPU: the same
-    lengths, caches and logits within bf16 rounding, also after decode steps fed the same
-    tokens."""
+    """Ragged prompts prefilled together (one packed forward writing each prompt's K/V in place,
+    PackedPrefill and the varlen operator) against the reference's flow of one prefill and
+    prefill_row per prompt, bf16 on the GPU: the same lengths, caches and logits within bf16
+    rounding, also after decode steps fed the same tokens."""
     _note("batched multi-prompt prefill")
     cfg = mixed_window_config(n_layer=4)
     mgr = gpu_manager(torch.bfloat16)
@@ -407,12 +409,19 @@ def test_batched_multi_prompt_prefill_matches_one_prefill_per_prompt():
     assert dec.kv_cache.cache_seqlens.tolist() == ref.cache_seqlens.tolist()
     for r, n in enumerate(ref.cache_seqlens.tolist()):
         for a, b in ((dec.kv_cache.k_cache, ref.k_cache), (dec.kv_cache.v_cache, ref.v_cache)):
-            assert (a[:, r, :n].float() - b[:, r, :n].float()).abs().max() <= 0.1, r
+            # the packed path runs RoPE / QK-norm / x1.2 as separate ops, the per-prompt path
+            # fused: within one bf16 unit of values up to ~4
+            err = (a[:, r, :n].float() - b[:, r, :n].float()).abs().max().item()
+            assert err <= 0.04, (r, err)
     want = torch.cat(ref_logits).repeat_interleave(S, 0).float()
-    assert (dec.logits.float() - want).abs().max() <= 0.1
+    err = (dec.logits.float() - want).abs().max().item()
+    print(f"prefill logits max-abs {err:.2e}", flush=True)
+    assert err <= 2e-3
     feed = torch.randint(0, cfg.vocab_size, (steps, len(prompts) * S), generator=g).to(DEV)
     with torch.no_grad():
         for t in range(steps):
             a = dec.step(feed[t]).float()
             b = model(feed[t].view(-1, 1), kv_cache=ref)[:, -1].float()
-            assert (a - b).abs().max() <= 0.1, t
+            err = (a - b).abs().max().item()
+            print(f"step {t}: logits max-abs {err:.2e}", flush=True)
+            assert err <= 2e-3, t

@@ -199,8 +199,9 @@ def test_the_default_operator_refuses_cpu_tensors():
 
 
 def test_batched_prompt_prefill_equals_one_prefill_per_prompt():
-    """The Decoder's batched prefill (prompts right-padded to the longest, then prefill_rows)
-    leaves the caches and first logits the reference's per-prompt prefill + prefill_row leave
+    """The Decoder's batched prefill (one packed forward writing each prompt's K/V in place,
+    then copies into the other sample rows) leaves the caches and first logits the reference's
+    per-prompt prefill + prefill_row leave
     (modelcore/generate.py:67-80), within fp32 rounding; rows end at their own lengths."""
     mgr = manager()
     model = awake(mgr.create_model(tiny_config(kv_share=True), device=CPU, seed=0))
@@ -240,6 +241,55 @@ def test_prefill_rows_refuses_what_it_cannot_place():
     dst.advance(1)
     with pytest.raises(AssertionError, match="non-empty"):
         dst.prefill_rows(src, [3, 6], 1)
+
+
+def test_packed_prefill_refuses_what_it_cannot_place():
+    from modelcore_amd.cache import PackedPrefill
+    mgr = manager()
+    model = mgr.create_model(tiny_config(), device=CPU, seed=0)
+    cache = mgr.new_kv_cache(model, batch_size=4, seq_len=8)
+    with pytest.raises(AssertionError, match="distinct"):
+        PackedPrefill(cache, [1, 1], [3, 4])
+    with pytest.raises(AssertionError, match="out of range"):
+        PackedPrefill(cache, [0, 4], [3, 4])
+    with pytest.raises(AssertionError, match="empty prompt"):
+        PackedPrefill(cache, [0, 1], [3, 0])
+    with pytest.raises(AssertionError, match="exceeds cache length"):
+        PackedPrefill(cache, [0, 1], [3, 9])
+    cache.cache_seqlens[2] = 5
+    cache._pos_uniform = None
+    with pytest.raises(AssertionError, match="non-empty"):
+        PackedPrefill(cache, [0, 2], [3, 4])
+    PackedPrefill(cache, [0, 3], [3, 4])  # rows 0 and 3 are empty: accepted
+
+
+def test_packed_prefill_moves_each_row_to_its_prompts_length():
+    """A packed forward over prompts placed in rows 3 and 1 of a 4-row cache: those rows end at
+    their prompts' lengths, the others stay empty (ragged host mirror); covering every row with
+    equal lengths leaves the cache uniform. The last-token logits equal each prompt's own."""
+    from modelcore_amd.cache import PackedPrefill
+    mgr = manager()
+    model = awake(mgr.create_model(tiny_config(kv_share=True), device=CPU, seed=0))
+    cache = mgr.new_kv_cache(model, batch_size=4, seq_len=12)
+    prompts = [[4, 8, 15, 16], [23, 42]]
+    packed = PackedPrefill(cache, [3, 1], [4, 2])
+    with torch.no_grad():
+        logits = model.last_logits(torch.tensor([prompts[0] + prompts[1]]), packed, None)
+    assert cache.cache_seqlens.tolist() == [0, 2, 0, 4] and cache.uniform_pos() is None
+    for p, prompt in enumerate(prompts):
+        one = mgr.new_kv_cache(model, batch_size=1, seq_len=len(prompt))
+        with torch.no_grad():
+            want = model(torch.tensor([prompt]), kv_cache=one)[:, -1]
+        torch.testing.assert_close(logits[p:p + 1], want, rtol=1e-5, atol=1e-6)
+        row = [3, 1][p]
+        n = len(prompt)
+        torch.testing.assert_close(cache.k_cache[:, row, :n], one.k_cache[:, 0, :n], rtol=1e-5,
+                                   atol=1e-6)
+    full = mgr.new_kv_cache(model, batch_size=2, seq_len=12)
+    with torch.no_grad():
+        model.last_logits(torch.tensor([[1, 2, 3, 4, 5, 6]]), PackedPrefill(full, [1, 0], [3, 3]),
+                          None)
+    assert full.uniform_pos() == 3 and full.cache_seqlens.tolist() == [3, 3]
 
 
 def test_interleaved_gate_up_weights_split_back_into_gate_and_up():

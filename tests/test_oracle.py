@@ -84,6 +84,38 @@ def test_oracle_matches_reference_sdpa_fallback(seqlens, T_new, H, H_kv, D, wind
     assert np.array_equal(kc, to_np(kc_t)) and np.array_equal(vc, to_np(vc_t))
 
 
+def test_varlen_restatement_matches_brute_force_per_sequence():
+    """The varlen form of the fallback (sequences packed along one token axis, each in its own
+    cache row at that row's position) against pure-Python brute force per sequence, and the
+    appends at each row's own positions; rows not listed keep their contents."""
+    g = gen(5)
+    B_cache, T_max, H, H_kv, D = 4, 20, 4, 2, 8
+    kc = randn(g, B_cache, T_max, H_kv, D, dtype=torch.float64)
+    vc = randn(g, B_cache, T_max, H_kv, D, dtype=torch.float64)
+    rows, bases, lengths = [2, 0, 3], [4, 0, 9], [3, 6, 1]
+    total = sum(lengths)
+    q = randn(g, total, H, D, dtype=torch.float64)
+    k = randn(g, total, H_kv, D, dtype=torch.float64)
+    v = randn(g, total, H_kv, D, dtype=torch.float64)
+    seqlens = torch.zeros(B_cache, dtype=torch.int32)
+    seqlens[rows] = torch.tensor(bases, dtype=torch.int32)
+    cu = torch.tensor([0, 3, 9, 10], dtype=torch.int32)
+    kc2, vc2 = kc.clone(), vc.clone()
+    y = sf.flash_attn_varlen_with_kvcache(q, kc2, vc2, k, v, seqlens.clone(), cu, 6,
+                                          torch.tensor(rows, dtype=torch.int32),
+                                          window_size=(4, 0))
+    a = 0
+    for r, s0, n in zip(rows, bases, lengths):
+        want_k, want_v = kc[r].clone(), vc[r].clone()
+        want_k[s0:s0 + n], want_v[s0:s0 + n] = k[a:a + n], v[a:a + n]
+        assert torch.equal(kc2[r], want_k) and torch.equal(vc2[r], want_v)
+        want = brute_force(to_np(q[a:a + n])[None], to_np(want_k)[None], to_np(want_v)[None],
+                           [s0], 4)[0]
+        np.testing.assert_allclose(to_np(y[a:a + n]), want, atol=1e-10, rtol=0)
+        a += n
+    assert torch.equal(kc2[1], kc[1]) and torch.equal(vc2[1], vc[1])
+
+
 def test_window_zero_returns_each_rows_own_value():
     """w = 0: every query sees only itself, so the output is its own V row exactly."""
     seqlens, T_new, H, H_kv = [3, 10], 4, 4, 2
