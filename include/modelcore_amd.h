@@ -21,6 +21,9 @@
  * col <= p and (window < 0 or p - col <= window); softmax scale is 1/sqrt(D); query head h reads
  * KV head h / (H / H_kv).
  *
+ * Attention takes head dims D with D * itemsize a multiple of 16, up to 512 (MCAMD_EUNSUPPORTED
+ * past that, before anything is launched).
+ *
  * A row whose positions fall outside [0, T_max) is not written by the append and gets NaN
  * attention output instead of an out-of-bounds access (the reference raises an index error there;
  * kernels cannot raise without a host sync).

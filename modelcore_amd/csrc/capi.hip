@@ -32,6 +32,8 @@ int check_attn_shapes(const AttnArgs &a, bool need_workspace) {
     return fail(MCAMD_EINVAL, "attention: tensors must be 16-byte aligned");
   if ((a.head_dim * int64_t(elem)) % 16 != 0)
     return fail(MCAMD_EUNSUPPORTED, "attention: head_dim * itemsize must be a multiple of 16");
+  if (head_dim_bucket(a.head_dim) == 0)
+    return fail(MCAMD_EUNSUPPORTED, "attention: head_dim must be at most 512");
   if (need_workspace) {
     const size_t need =
         decode_workspace_bytes(a.batch, a.n_head, a.n_kv_head, a.head_dim, a.t_max, a.window);

@@ -159,7 +159,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // The power of two (16 to 256) whose kernel instantiation serves head_dim d, or 0 past 256.
 inline int head_dim_bucket(int64_t d) {
-  if (d > 256) return 0;
+  if (d > 512) return 0;
   int p = 16;
   while (p < d) p *= 2;
   return p;

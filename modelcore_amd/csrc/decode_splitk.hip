@@ -264,7 +264,8 @@ int dispatch_gm(DecodeParams &P, int B, hipStream_t s) {
   return run_decode<E, DP, 8>(P, B, s);
 }
 
-// Any head_dim up to 256 whose rows are whole 16-byte vectors (checked before), run in the
+// Any head_dim up to 256 whose rows are whole 16-byte vectors (checked before; wider heads take
+// the general prefill kernel, see launch_decode), run in the
 // instantiation of the next power of two.
 template <class E>
 int dispatch_d(DecodeParams &P, int B, hipStream_t s) {
@@ -289,7 +290,8 @@ int64_t decode_max_splits(int64_t t_max, int64_t window) {
 size_t decode_workspace_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
                               int64_t t_max, int64_t window) {
   const int64_t ns = decode_max_splits(t_max, window);
-  const size_t generic = size_t(batch * n_head * ns * (head_dim + 2) * 4);
+  // Head dims above 256 take the general prefill kernel, which needs no workspace.
+  const size_t generic = head_dim > 256 ? 0 : size_t(batch * n_head * ns * (head_dim + 2) * 4);
   // The fused path serves head_dim 128 (bf16); other head dims only ever take the general one.
   const size_t fused =
       head_dim == 128 ? decode_fused_partial_bytes(batch, n_head, n_kv_head, t_max, window) : 0;
@@ -313,6 +315,15 @@ int launch_decode(const AttnArgs &a) {
                   a.dtype, a.stream};
     st = launch_append(ap);
     if (st != MCAMD_OK) return st;
+  }
+  if (a.head_dim > 256) {
+    // One key row is more than a wave's 64 lanes of 16 bytes: the general prefill kernel (one
+    // query per row here) walks the keys instead, with no split and no workspace.
+    AttnArgs pa = a;
+    pa.k_new = pa.v_new = nullptr;  // appended above
+    st = launch_prefill_generic(pa);
+    if (st != MCAMD_OK || !a.advance_seqlens) return st;
+    return launch_advance(a.advance_seqlens, a.batch, a.advance, a.stream);
   }
   DecodeParams P;
   P.q = a.q;

@@ -105,6 +105,10 @@ int64_t decode_fused_units(int64_t n_head, int64_t n_kv_head);
 size_t decode_fused_partial_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head,
                                   int64_t t_max, int64_t window);
 
+// The general chunked prefill (any dtype, head_dim up to 512); it also serves single-token
+// calls with head_dim above 256, past what the split-K decode kernel takes.
+int launch_prefill_generic(const AttnArgs &a);
+
 // The bf16 / head_dim 128 chunked prefill on the matrix cores.
 bool prefill_mfma_supported(const AttnArgs &a);
 int launch_prefill_mfma(const AttnArgs &a);

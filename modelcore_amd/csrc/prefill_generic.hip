@@ -23,7 +23,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kRows = 64;
-constexpr int KT = 32;
+// Keys per LDS tile: 32, or 16 for head dims above 256 (K and V tiles of 64 KiB in fp32).
+template <int DP>
+constexpr int kTileKeys = DP <= 256 ? 32 : 16;
 
 struct PrefillParams {
   const void *q, *k_cache, *v_cache;
@@ -38,6 +40,7 @@ struct PrefillParams {
 template <class E, int DP>
 __global__ __launch_bounds__(kThreads) void prefill_generic_kernel(PrefillParams P) {
   constexpr int DS = DP / 4;  // dimensions per lane (lane j owns d = 4*i + j, d < DP)
+  constexpr int KT = kTileKeys<DP>;
   constexpr int VEC = Vec<E>::N;
   const int D = P.D;          // the real head_dim (<= DP); dims past it are zero in LDS and q
   __shared__ float sk[KT][DP];
@@ -177,8 +180,9 @@ int dispatch_d(const PrefillParams &P, int D, int B, hipStream_t s) {
     case 64: return run_prefill<E, 64>(P, B, s);
     case 128: return run_prefill<E, 128>(P, B, s);
     case 256: return run_prefill<E, 256>(P, B, s);
+    case 512: return run_prefill<E, 512>(P, B, s);
     default:
-      return fail(MCAMD_EUNSUPPORTED, "prefill: head_dim must be at most 256");
+      return fail(MCAMD_EUNSUPPORTED, "attention: head_dim must be at most 512");
   }
 }
 

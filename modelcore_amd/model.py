@@ -345,7 +345,8 @@ class Attention(nn.Module):
         each row's position from cache_seqlens on the device (the separate ops slice the tables
         at the host-side position instead)."""
         return kv_cache is not None and self.epilogue is not None and self.fuse_epilogue \
-            and isinstance(self.norm, RMSNorm) and not isinstance(kv_cache, PackedPrefill)
+            and isinstance(self.norm, RMSNorm) and not isinstance(kv_cache, PackedPrefill) \
+            and self.head_dim <= 256  # the fused step's kernel covers head dims up to 256
 
     def forward(self, x, kv_cache, kv_bus):
         B, T, _ = x.size()

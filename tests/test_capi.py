@@ -183,15 +183,22 @@ def test_decode_loop_entry_points_reject_bad_shapes_before_any_launch():
     assert b"token stride" in lib.mcamd_last_error()
 
 
-def test_head_dims_past_256_are_refused_before_any_launch():
-    """Any head_dim of whole 16-byte rows up to 256 runs (the power-of-two kernel above it, with
-    idle lanes); wider heads have no kernel and say so without touching the GPU."""
+def test_head_dims_past_512_are_refused_before_any_launch():
+    """Any head_dim of whole 16-byte rows up to 512 runs (the power-of-two kernel above it, with
+    idle lanes); wider heads have no kernel and say so without touching the GPU -- also the
+    operator with new k/v, whose append would otherwise run first."""
     lib = _ext.lib()
     fake = 1 << 20  # never dereferenced
-    D, T_max = 384, 64
+    D, T_max = 640, 64
     st = lib.mcamd_decode_attention(fake, fake, fake, fake, fake, 2, 8, 4, D, T_max,
                                     T_max * 4 * D, -1, _ext.BF16, fake, 1 << 40, None)
-    assert st == _ext.EUNSUPPORTED and b"at most 256" in lib.mcamd_last_error()
+    assert st == _ext.EUNSUPPORTED and b"at most 512" in lib.mcamd_last_error()
     st = lib.mcamd_prefill_attention(fake, fake, fake, fake, fake, 2, 5, 8, 4, D, T_max,
                                      T_max * 4 * D, -1, _ext.BF16, None)
-    assert st == _ext.EUNSUPPORTED and b"at most 256" in lib.mcamd_last_error()
+    assert st == _ext.EUNSUPPORTED and b"at most 512" in lib.mcamd_last_error()
+    st = lib.mcamd_flash_attn_with_kvcache(fake, fake, fake, fake, fake, fake, fake, 2, 1, 8, 4,
+                                           D, T_max, T_max * 4 * D, -1, 1, _ext.BF16, fake,
+                                           1 << 40, None)
+    assert st == _ext.EUNSUPPORTED and b"at most 512" in lib.mcamd_last_error()
+    # head dims above 256 need no decode workspace: they take the general prefill kernel
+    assert lib.mcamd_attn_workspace_bytes(2, 1, 8, 4, 384, T_max, -1) == 0

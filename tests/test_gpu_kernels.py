@@ -200,6 +200,10 @@ DECODE_CASES = [
     ([100, 7], 12, 4, 96, 128, 33),
     ([300, 5, 77], 8, 2, 192, 320, -1),
     ([60, 3], 4, 4, 48, 64, -1),
+    # head dims above 256 (up to 512): the general prefill kernel with one query per row
+    ([37, 300, 0, 5], 8, 2, 512, 320, -1),
+    ([100, 7], 6, 2, 384, 128, 33),
+    ([31], 4, 1, 320, 40, -1),
 ]
 
 
@@ -297,6 +301,8 @@ PREFILL_CASES = [
     ([17, 3], 25, 16, 4, 80, 64, -1),             # head dims that are not powers of two
     ([100, 0, 31], 70, 12, 4, 96, 200, 50),
     ([5, 40], 33, 8, 2, 192, 80, -1),
+    ([17, 3], 25, 8, 2, 384, 64, -1),             # head dims above 256, up to 512
+    ([100, 0], 20, 4, 4, 512, 140, 50),
 ]
 
 

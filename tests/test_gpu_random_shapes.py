@@ -23,7 +23,7 @@ def _draw(i):
     dtype = torch.bfloat16 if r.random() < 0.75 else torch.float32
     H_kv = int(r.choice([1, 2, 4, 8]))
     G = int(r.choice([1, 2, 3, 4, 8, 16]))
-    D = int(r.choice([16, 48, 64, 80, 96, 128, 128, 128, 192, 256]))
+    D = int(r.choice([16, 48, 64, 80, 96, 128, 128, 128, 192, 256, 384, 512]))
     T_new = 1 if r.random() < 0.6 else int(r.integers(2, 71))
     B = int(r.choice([1, 2, 3, 5, 16, 33, 70])) if T_new == 1 else int(r.integers(1, 4))
     T_max = int(r.integers(T_new + 8, 1500 if T_new == 1 else 700))
