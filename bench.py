@@ -74,7 +74,9 @@ def parse_args():
     ap.add_argument("--decode-only", action="store_true",
                     help="default workload: time the decode microbench only, without the "
                          "prefill, mixed-window and replication objects")
-    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
+    ap.add_argument("--eager", action="store_true",
+                    help="decode and mixed workloads: time eager launches instead of a graph "
+                         "(the counter runs)")
     ap.add_argument("--library-gemm", action="store_true",
                     help="sample workload: run the decode projections through F.linear (the "
                          "library GEMM) instead of mcamd_linear_bf16")
@@ -104,6 +106,13 @@ def parse_args():
                     help="print the traffic summary of the decode call from rocprofv3 --pmc "
                          "FETCH_SIZE and WRITE_SIZE runs of `bench.py --eager --no-cpu-baseline` and "
                          "of `bench.py --calibrate-copy` (counter_collection.csv files)")
+    ap.add_argument("--summarize-counters", nargs=7,
+                    metavar=("WORKLOAD", "FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE", "UNITS",
+                             "ALGO_BYTES"),
+                    help="print the traffic summary of workload prefill, mixed or replicate from "
+                         "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of it (its last UNITS "
+                         "passes, steps or launches, ALGO_BYTES algorithmic bytes each) and of "
+                         "bench.py --calibrate-copy")
     ap.add_argument("--summarize-trace", metavar="CSV",
                     help="print the mean duration of the decode call's kernels over the last "
                          "--launches dispatches of a rocprofv3 kernel_trace.csv")
@@ -252,6 +261,104 @@ def calibrate_copy():
 
 PF_B, PF_T, PF_C, PF_H, PF_HKV = 8, 16384, 512, 32, 8
 
+# Committed counter summaries of the other workloads: kernels summed, the unit the traffic is
+# given per, and how many of those units the counter run's last dispatches cover.
+TRAFFIC_PROFILES = {
+    "prefill": dict(file="profiles/prefill_b8_t16384_c512_gqa32x8_hd128_traffic.md",
+                    kernels=("prefill_mfma_kernel",), unit="pass", dispatches_per_unit=32),
+    "mixed": dict(file="profiles/mixed_l24_b16_ctx4096_gqa12x4_hd128_traffic.md",
+                  kernels=("decode_fused_kernel", "decode_merge_kernel"), unit="step",
+                  dispatches_per_unit=48),
+    "replicate": dict(file="profiles/replicate_s32_p2048_r64_hkv8_hd128_traffic.md",
+                      kernels=("kv_replicate_kernel",), unit="launch", dispatches_per_unit=1),
+}
+
+
+def profile_traffic(name, bytes_now):
+    """(HBM bytes per unit of workload `name`, where the figure comes from) from its committed
+    counter summary, scaled by the summary's traffic/bytes ratio when it was measured at other
+    algorithmic bytes (said so); (None, reason) without one."""
+    import re
+    spec = TRAFFIC_PROFILES[name]
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), spec["file"])
+    try:
+        with open(path) as f:
+            text = f.read()
+    except OSError:
+        return None, f"{spec['file']} missing"
+    t = re.search(r"^traffic_bytes_per_unit:\s*(\d+)", text, re.M)
+    a = re.search(r"^algorithmic_bytes_per_unit:\s*(\d+)", text, re.M)
+    if not (t and a):
+        return None, f"{spec['file']} holds no per-{spec['unit']} figures"
+    traffic, algo = int(t.group(1)), int(a.group(1))
+    how = (f"{spec['file']}: rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE (copy-calibrated) of "
+           f"{' + '.join(spec['kernels'])}, per {spec['unit']}")
+    if algo == bytes_now:
+        return traffic, how
+    return round(traffic / algo * bytes_now), how + (f", measured at {algo} algorithmic bytes and "
+                                                     f"scaled by its ratio {traffic / algo:.4f}")
+
+
+def summarize_counters(name, fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, units,
+                       algo_bytes):
+    """Markdown traffic summary of workload `name` from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    runs (the last `units` units' dispatches of its kernels) and of the plain copy; ends with the
+    two lines profile_traffic reads."""
+    import statistics as st
+    spec = TRAFFIC_PROFILES[name]
+
+    def copy_scale(rows, counter):
+        vals = [float(r["Counter_Value"]) for r in rows
+                if r["Counter_Name"] == counter and "copyBuffer" in r["Kernel_Name"]]
+        kib = st.median(vals)
+        return kib, COPY_BYTES / 1024 / kib
+
+    def kernel_sum(rows, counter):
+        vals = [(int(r["Dispatch_Id"]), float(r["Counter_Value"])) for r in rows
+                if r["Counter_Name"] == counter and
+                any(k in r["Kernel_Name"] for k in spec["kernels"])]
+        vals.sort()
+        last = vals[-units * spec["dispatches_per_unit"]:]
+        return sum(v for _, v in last), len(last)
+
+    cf_kib, cf_scale = copy_scale(_counter_rows(copy_fetch_csv), "FETCH_SIZE")
+    cw_kib, cw_scale = copy_scale(_counter_rows(copy_write_csv), "WRITE_SIZE")
+    fk, n_f = kernel_sum(_counter_rows(fetch_csv), "FETCH_SIZE")
+    wk, n_w = kernel_sum(_counter_rows(write_csv), "WRITE_SIZE")
+    per_unit = (fk * cf_scale + wk * cw_scale) * 1024 / units
+    print(f"Calibration (plain device copy of {COPY_BYTES >> 20} MiB): FETCH_SIZE reads "
+          f"{cf_kib:.1f} KiB per launch (scale {cf_scale:.3f}), WRITE_SIZE {cw_kib:.1f} KiB "
+          f"(scale {cw_scale:.3f}).\n")
+    plural = {"pass": "passes", "launch": "launches", "step": "steps"}[spec["unit"]]
+    print(f"{' + '.join(spec['kernels'])}: the last {units} {plural} ({n_f} / {n_w} "
+          f"dispatches): FETCH_SIZE {fk / units:.1f} KiB, WRITE_SIZE {wk / units:.1f} KiB per "
+          f"{spec['unit']}, scaled: {per_unit:.0f} bytes against {algo_bytes} algorithmic "
+          f"bytes ({per_unit / algo_bytes:.3f}x).\n")
+    print(f"traffic_bytes_per_unit: {round(per_unit)}")
+    print(f"algorithmic_bytes_per_unit: {algo_bytes}")
+
+
+def prefill_pass_bytes():
+    """Bytes one attention pass of the chunked prefill must move at least: each chunk reads its
+    row's K/V prefix (chunk included) once per KV head and the chunk's q, and writes its out."""
+    total = 0
+    for c in range(PF_T // PF_C):
+        keys = (c + 1) * PF_C
+        total += PF_B * keys * PF_HKV * D * 2 * 2 + 2 * PF_B * PF_C * PF_H * D * 2
+    return total
+
+
+def mixed_step_bytes(first, steps):
+    """Mean algorithmic bytes of `steps` mixed-stack steps from position 4096 + first."""
+    from modelcore_amd import stats
+    windows = [-1 if i % 4 == 3 else MX_WIN for i in range(MX_LAYERS)]
+    total = 0
+    for s in range(steps):
+        pos = [MX_P + first + s] * MX_B
+        for w in windows:
+            total += stats.decode_step_bytes(pos, MX_H, MX_HKV, D, 2, window=w)
+    return total // steps
+
 
 def bench_prefill(args):
     """Chunked prefill: 8 rows x 16384 tokens fed in 32 chunks of 512; each chunk appends its K/V
@@ -369,7 +476,7 @@ def bench_prefill(args):
                      "achieved": round(achieved / 1e12, 1), "peak": flops_peak / 1e12,
                      "peak_source": peak_src,
                      "unit": "TFLOP/s", "frac": round(achieved / flops_peak, 4),
-                     "traffic": None, "ms_per_pass": round(attn_ms, 4), "flops_per_pass": flops},
+                     "ms_per_pass": round(attn_ms, 4), "flops_per_pass": flops},
         "append": {"kernel": "kv_append_kernel (K/V copy of the 32 chunks)", "bound": "hbm",
                    "achieved": round(append_bw / 1e9, 1), "peak": bw_peak / 1e9, "unit": "GB/s",
                    "frac": round(append_bw / bw_peak, 4), "ms_per_pass": round(append_ms, 4),
@@ -377,6 +484,13 @@ def bench_prefill(args):
                    "traffic_source": append_traffic_src,
                    "bytes_per_launch": append_bytes // n_chunks},
     }
+    # Traffic of the attention pass: K/V of each chunk's prefix, q and out (the algorithmic
+    # bytes a pass must move at least: every key read once per (row, KV head), not once per query
+    # tile), against what the counters measured.
+    pf_bytes = prefill_pass_bytes()
+    t, src = profile_traffic("prefill", pf_bytes)
+    result["roofline"].update({"traffic": t, "traffic_unit": "bytes per pass",
+                               "traffic_min_bytes": pf_bytes, "traffic_source": src})
     if not args.no_cpu_baseline:
         log("CPU baseline: the whole chunked prefill on host cores")
         result["cpu_baseline"] = cpu_prefill_baseline(q, k, v)
@@ -459,9 +573,11 @@ def bench_replicate(args):
                    "head_dim": D},
         "roofline": {"kernel": "kv_replicate_kernel", "bound": "hbm", "achieved": round(gbps, 1),
                      "peak": hbm_peak / 1e9, "peak_source": peak_src, "unit": "GB/s",
-                     "frac": round(gbps * 1e9 / hbm_peak, 4),
-                     "traffic": None, "bytes_per_launch": nbytes},
+                     "frac": round(gbps * 1e9 / hbm_peak, 4), "bytes_per_launch": nbytes},
     }
+    t, src = profile_traffic("replicate", nbytes)
+    result["roofline"].update({"traffic": t, "traffic_unit": "bytes per launch",
+                               "traffic_source": src})
     if not args.no_cpu_baseline:
         log("CPU baseline: the replication's broadcast copy on host cores")
         result["cpu_baseline"] = cpu_replicate_baseline(src)
@@ -544,27 +660,28 @@ def bench_mixed(args):
     for s in range(W):
         step(s)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if args.eager:  # (the counter runs: one dispatch per kernel, in program order)
+        start.record()
         for s in range(K):
             step(W + s)
-    # One untimed replay (a graph's first launch also uploads it), then the positions set back:
-    # the timed replay rewrites the same new tokens at the same positions.
-    graph.replay()
-    torch.cuda.synchronize()
-    cache.cache_seqlens.fill_(MX_P + W)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    graph.replay()
-    end.record()
+        end.record()
+    else:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for s in range(K):
+                step(W + s)
+        # One untimed replay (a graph's first launch also uploads it), then the positions set
+        # back: the timed replay rewrites the same new tokens at the same positions.
+        graph.replay()
+        torch.cuda.synchronize()
+        cache.cache_seqlens.fill_(MX_P + W)
+        start.record()
+        graph.replay()
+        end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / K
-    total = 0
-    for s in range(K):
-        pos = [MX_P + W + s] * MX_B
-        for w in windows:
-            total += stats.decode_step_bytes(pos, MX_H, MX_HKV, D, 2, window=w)
-    step_bytes = total / K
+    step_bytes = mixed_step_bytes(W, K)
     gbps = step_bytes / (ms * 1e-3) / 1e9
     hbm_peak, _, peak_src = peaks()
     result = {
@@ -576,15 +693,19 @@ def bench_mixed(args):
         "config": {"workload": "KV path of one decode step of a 24-layer stack (18 layers window "
                                "1024, 6 global; odd layers share the previous layer's slot), B=16, "
                                "positions 4096+", "layers": MX_LAYERS, "batch": MX_B,
-                   "n_head": MX_H, "n_kv_head": MX_HKV, "head_dim": D, "timing": "hip_graph",
+                   "n_head": MX_H, "n_kv_head": MX_HKV, "head_dim": D,
+                   "timing": "eager" if args.eager else "hip_graph",
                    "advance": "in the last call's merge pass (advance=1)" if fold
                               else "KVCache.advance launch"},
         "roofline": {"kernel": "decode_fused_kernel + decode_merge_kernel (24 calls per step)",
                      "bound": "hbm", "achieved": round(gbps, 1), "peak": hbm_peak / 1e9,
                      "peak_source": peak_src, "unit": "GB/s",
-                     "frac": round(gbps * 1e9 / hbm_peak, 4), "traffic": None,
+                     "frac": round(gbps * 1e9 / hbm_peak, 4),
                      "bytes_per_step": int(step_bytes)},
     }
+    t, src = profile_traffic("mixed", int(step_bytes))
+    result["roofline"].update({"traffic": t, "traffic_unit": "bytes per step",
+                               "traffic_source": src})
     if not args.no_cpu_baseline:
         log("CPU baseline: whole steps of the stack (24 calls) on host cores")
         result["cpu_baseline"] = cpu_mixed_baseline(cache, qs, ks, vs, windows, W)
@@ -874,6 +995,10 @@ def main():
         return
     if args.summarize_trace:
         summarize_trace(args.summarize_trace, args.launches)
+        return
+    if args.summarize_counters:
+        name, f, w, cf, cw, units, algo = args.summarize_counters
+        summarize_counters(name, f, w, cf, cw, int(units), int(algo))
         return
     if args.calibrate_copy:
         calibrate_copy()

@@ -317,7 +317,8 @@ int launch_decode(const AttnArgs &a) {
     if (st != MCAMD_OK) return st;
   }
   if (a.head_dim > 256) {
-    // One key row is more than a wave's 64 lanes of 16 bytes: the general prefill kernel (one
+    // Past 256 an fp32 key row needs more than a wave's 64 lanes of 16 bytes, and the cross-wave
+    // sum buffer (4 x GM x D floats) outgrows the LDS budget: the general prefill kernel (one
     // query per row here) walks the keys instead, with no split and no workspace.
     AttnArgs pa = a;
     pa.k_new = pa.v_new = nullptr;  // appended above
