@@ -43,8 +43,8 @@
 //  * Shared prefix: when the caller states that every row's keys [0, S) are copies of row 0's
 //    (rows replicated from one prompt), those keys come from row 0 for every row. A wide batch
 //    with no window (at least 64 (row, query head) pairs per KV head, S >= 512) takes them on the
-//    matrix cores first (the chunked-prefill kernel in its prefix mode: every row's queries
-//    against row 0's keys, in up to sixteen key ranges, as partial slots of each unit); this pass
+//    matrix cores first (prefix_mfma_kernel: every row's queries against row 0's keys, in key
+//    ranges sized to fill the chip, one partial slot of each unit per range); this pass
 //    then covers each row's keys from S on and writes partials even for a single segment, and
 //    the merge folds the prefix partials in (sums in another order: within bf16 rounding of the
 //    unshared call). Otherwise this pass reads the keys below S from row 0 itself: the same
@@ -105,10 +105,6 @@ constexpr int kBucket = MCAMD_DECODE_BUCKET;
 constexpr int kSpec = MCAMD_DECODE_SPEC;
 constexpr int64_t kTemporalLimit = int64_t(64) << 20;  // bytes of K/V: see launch_decode_fused
 constexpr int64_t kPrefixMinKeys = 512;       // shorter shared prefixes stay in this pass
-#ifndef MCAMD_PREFIX_KEYS
-#define MCAMD_PREFIX_KEYS 128
-#endif
-constexpr int64_t kPrefixKeysPerSplit = MCAMD_PREFIX_KEYS;  // keys per matrix-core workgroup, at least
 static_assert(kSpec <= kBucket, "speculative merge loads stay inside the unit's bucket");
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -680,11 +676,11 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(
 // follow BATCH at a time. The pass does not read cache_seqlens (the descriptors carry all it
 // needs), so it can also advance the positions: the wave of each row's first unit and head adds
 // `advance` to the row's entry.
-// PRE: also fold in the unit's n_pre partials of the shared prefix (loaded with the rest, in
-// the same round trip); a unit's single segment is then a partial too.
+// NP > 0: also fold in the unit's n_pre <= NP partials of the shared prefix (loaded with the
+// rest, in the same round trip); a unit's single segment is then a partial too.
 // As for the streaming pass, the leading arguments are the fields of P the pass needs first,
 // passed separately so that they arrive preloaded in SGPRs.
-template <int SPEC, bool PRE>
+template <int SPEC, int NP>
 __global__ __launch_bounds__(64) void decode_merge_kernel(
     const float *__restrict__ a_part, const int2 *__restrict__ a_desc, uint16_t *a_out,
     int32_t *a_adv, int a_n_units, int a_n_hc, int a_H_kv, int a_G, int a_H, int a_advance,
@@ -727,8 +723,8 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
     ml[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * hr);
     v[k] = *reinterpret_cast<const float2 *>(ps + hr * D + 2 * lane);
   }
-  constexpr int NP = PRE ? kPrefixMaxSplits : 1;
-  float2 pml[NP], pv[NP];
+  constexpr bool PRE = NP > 0;
+  float2 pml[PRE ? NP : 1], pv[PRE ? NP : 1];
   if constexpr (PRE) {
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
@@ -876,7 +872,8 @@ int launch_decode_fused(const AttnArgs &a) {
   const size_t pre_ws =
       decode_prefix_bytes(a.batch, a.n_head, a.n_kv_head, a.head_dim, a.t_max, a.window);
   if (pre_ws > 0 && a.shared_prefix >= kPrefixMinKeys && a.workspace_bytes >= base_ws + pre_ws) {
-    P.n_pre = int(std::min<int64_t>(kPrefixMaxSplits, a.shared_prefix / kPrefixKeysPerSplit));
+    P.n_pre = prefix_partial_splits(a.batch, a.n_head, a.n_kv_head, a.shared_prefix,
+                                    device_cus(), kPrefixMaxSplits);
     P.lo_floor = int(a.shared_prefix);
     float *pre = reinterpret_cast<float *>(ws + base_ws);
     P.pre = pre;
@@ -916,14 +913,16 @@ int launch_decode_fused(const AttnArgs &a) {
   };
   constexpr int S16 = kSpec < 16 ? kSpec : 16, S8 = kSpec < 8 ? kSpec : 8,
                 S4 = kSpec < 4 ? kSpec : 4;
-  if (P.n_pre > 0)
-    merge(decode_merge_kernel<S4, true>);
+  if (P.n_pre > 4)
+    merge(decode_merge_kernel<S4, kPrefixMaxSplits>);
+  else if (P.n_pre > 0)
+    merge(decode_merge_kernel<S4, 4>);
   else if (kSpec >= 16 && per_unit > 8)
-    merge(decode_merge_kernel<S16, false>);
+    merge(decode_merge_kernel<S16, 0>);
   else if (per_unit > 4)
-    merge(decode_merge_kernel<S8, false>);
+    merge(decode_merge_kernel<S8, 0>);
   else
-    merge(decode_merge_kernel<S4, false>);
+    merge(decode_merge_kernel<S4, 0>);
   return launch_status("decode_merge");
 }
 
