@@ -51,6 +51,7 @@ HIPCC_FLAGS = [
 # forth on every key tile (measured: ~500 v_accvgpr moves per tile).
 SOURCE_FLAGS = {
     "prefill_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "decode_fused.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],  # its shared-prefix jobs
 }
 
 

@@ -51,6 +51,7 @@
 //    values in the same order, the same results, with the rows' repeated reads of one row's
 //    lines served by L2 and the memory-side cache instead of HBM.
 #include "kernels.h"
+#include "prefix_mfma.h"
 
 #include <atomic>
 
@@ -349,11 +350,14 @@ __device__ __forceinline__ int xcd_major(int id, int n) {
 // leading arguments, as many as fit the 14 free user SGPRs, stopping at the first aggregate):
 // scalar arguments only, hence the copies. The scan then starts without waiting for a kernel-argument load from memory
 // (measured: mixed-window step 0.394 -> 0.387 ms, decode call +0.3%, four paired runs).
-template <bool NT>
-__global__ __launch_bounds__(64 * NW) void decode_fused_kernel(
+// PX: workgroups n_groups and up run the shared prefix's matrix-core jobs instead (job
+// blockIdx.x - n_groups), two workgroups to a compute unit, so that the jobs run beside the
+// streaming workgroups.
+template <bool NT, bool PX>
+__device__ __forceinline__ void decode_fused_body(
     const int32_t *a_seqlens, const uint16_t *a_q, uint16_t *a_k_cache, uint16_t *a_v_cache,
     int a_B, int a_n_groups, int a_window, int a_lo_floor, int a_T_max, int a_n_units,
-    FusedParams P) {
+    FusedParams &P, const px::Params *X) {
   P.seqlens = a_seqlens;
   P.q = a_q;
   P.k_cache = a_k_cache;
@@ -364,7 +368,20 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(
   P.lo_floor = a_lo_floor;
   P.T_max = a_T_max;
   P.n_units = a_n_units;
-  __shared__ WaveAcc s_acc[NW];
+  WaveAcc *s_acc;
+  if constexpr (PX) {
+    static_assert(NW == px::kWaves, "the prefix jobs take one wave per SIMD, four per workgroup");
+    static_assert(sizeof(WaveAcc) * NW <= px::kLdsBytes, "the merge buffer fits the job's LDS");
+    __shared__ __attribute__((aligned(1024))) unsigned char s_raw[px::kLdsBytes];
+    if (int(blockIdx.x) >= P.n_groups) {
+      px::job(*X, int(blockIdx.x) - P.n_groups, s_raw);
+      return;
+    }
+    s_acc = reinterpret_cast<WaveAcc *>(s_raw);
+  } else {
+    __shared__ WaveAcc s_acc_own[NW];
+    s_acc = s_acc_own;
+  }
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;  // wave within the workgroup
   const int g = xcd_major(int(blockIdx.x), P.n_groups);
@@ -669,6 +686,27 @@ __global__ __launch_bounds__(64 * NW) void decode_fused_kernel(
   }
 }
 
+template <bool NT>
+__global__ __launch_bounds__(64 * NW) void decode_fused_kernel(
+    const int32_t *a_seqlens, const uint16_t *a_q, uint16_t *a_k_cache, uint16_t *a_v_cache,
+    int a_B, int a_n_groups, int a_window, int a_lo_floor, int a_T_max, int a_n_units,
+    FusedParams P) {
+  decode_fused_body<NT, false>(a_seqlens, a_q, a_k_cache, a_v_cache, a_B, a_n_groups, a_window,
+                               a_lo_floor, a_T_max, a_n_units, P, nullptr);
+}
+
+// The same pass with the shared prefix's jobs beside it: at most 256 registers per lane, so that
+// a job's workgroup and a streaming one share a compute unit.
+template <bool NT>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void
+decode_fused_prefix_kernel(const int32_t *a_seqlens, const uint16_t *a_q, uint16_t *a_k_cache,
+                           uint16_t *a_v_cache, int a_B, int a_n_groups, int a_window,
+                           int a_lo_floor, int a_T_max, int a_n_units, FusedParams P,
+                           px::Params X) {
+  decode_fused_body<NT, true>(a_seqlens, a_q, a_k_cache, a_v_cache, a_B, a_n_groups, a_window,
+                              a_lo_floor, a_T_max, a_n_units, P, &X);
+}
+
 // Merge pass with one wave per (unit, query head): lane l combines dims 2l, 2l+1 of that head
 // over the unit's segments. The loads of the unit's first SPEC bucket slots are issued with that
 // of its descriptor, before the segment count is known (one memory round trip for units of up to
@@ -867,21 +905,38 @@ int launch_decode_fused(const AttnArgs &a) {
   P.lo_floor = 0;
   P.pre = nullptr;
   P.n_pre = 0;
+  px::Params X{};  // the prefix jobs (P.n_pre > 0)
   const size_t base_ws =
       decode_workspace_bytes(a.batch, a.n_head, a.n_kv_head, a.head_dim, a.t_max, a.window);
   const size_t pre_ws =
       decode_prefix_bytes(a.batch, a.n_head, a.n_kv_head, a.head_dim, a.t_max, a.window);
   if (pre_ws > 0 && a.shared_prefix >= kPrefixMinKeys && a.workspace_bytes >= base_ws + pre_ws) {
-    P.n_pre = prefix_partial_splits(a.batch, a.n_head, a.n_kv_head, a.shared_prefix,
-                                    device_cus(), kPrefixMaxSplits);
+    P.n_pre = px::splits(a.batch, a.n_head, a.n_kv_head, a.shared_prefix, device_cus(),
+                         kPrefixMaxSplits);
     P.lo_floor = int(a.shared_prefix);
     float *pre = reinterpret_cast<float *>(ws + base_ws);
     P.pre = pre;
-    PrefixArgs pa{a.q,     a.k_cache,   a.v_cache, pre,
-                  a.batch, a.n_head,    a.n_kv_head, a.t_max,
-                  a.cache_batch_stride, a.shared_prefix, P.n_pre, a.stream};
-    const int st = launch_prefix_partials(pa);
-    if (st != MCAMD_OK) return st;
+    X.q = static_cast<const uint16_t *>(a.q);
+    X.k_cache = static_cast<const uint16_t *>(a.k_cache);
+    X.v_cache = static_cast<const uint16_t *>(a.v_cache);
+    X.part = pre;
+    X.H = P.H;
+    X.H_kv = P.H_kv;
+    X.G = P.G;
+    X.n_pairs = P.B * P.G;
+    X.n_pg = (X.n_pairs + 31) / 32;
+    X.n_split = P.n_pre;
+    X.key_len = int((a.shared_prefix + P.n_pre - 1) / P.n_pre);
+    X.prefix = int(a.shared_prefix);
+    X.n_units = P.n_units;
+    X.n_hc = P.n_hc;
+    X.T_max = P.T_max;
+    X.scale_log2 = P.scale_log2;
+    X.jobs = X.n_pg * P.H_kv * P.n_pre;
+    // Every key range holds keys: (n_pre - 1) * ceil(prefix / n_pre) < prefix, since at most
+    // sixteen ranges of at least 128 keys are made.
+    if (int64_t(P.n_pre - 1) * X.key_len >= a.shared_prefix)
+      return fail(MCAMD_EINVAL, "decode: empty shared-prefix key range");
   }
   // K/V bytes the call can read (every row at its longest span). A call that fits in a quarter
   // of the 256 MB memory-side cache loads them with the default policy, so a KV-sharing layer
@@ -890,14 +945,22 @@ int launch_decode_fused(const AttnArgs &a) {
   // stream non-temporal: allocating lines that no later read finds costs bandwidth (the decode
   // microbench's call with the default policy, alternating two caches: 57.3 against 49.8 us).
   const int64_t kv_bytes = int64_t(a.batch) * span * a.n_kv_head * D * 2 * 2;
-  if (kv_bytes <= kTemporalLimit)
-    hipLaunchKernelGGL(decode_fused_kernel<false>, dim3(unsigned(groups)), dim3(64 * NW), 0, a.stream,
+  auto stream_pass = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(unsigned(groups)), dim3(64 * NW), 0, a.stream, P.seqlens, P.q,
+                       P.k_cache, P.v_cache, P.B, P.n_groups, P.window, P.lo_floor, P.T_max,
+                       P.n_units, P);
+  };
+  // With a prefix on the matrix cores, its jobs are the grid's last workgroups.
+  auto prefix_pass = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(unsigned(groups + X.jobs)), dim3(64 * NW), 0, a.stream,
                        P.seqlens, P.q, P.k_cache, P.v_cache, P.B, P.n_groups, P.window,
-                       P.lo_floor, P.T_max, P.n_units, P);
+                       P.lo_floor, P.T_max, P.n_units, P, X);
+  };
+  const bool nt = kv_bytes > kTemporalLimit;
+  if (P.n_pre > 0)
+    nt ? prefix_pass(decode_fused_prefix_kernel<true>) : prefix_pass(decode_fused_prefix_kernel<false>);
   else
-    hipLaunchKernelGGL(decode_fused_kernel<true>, dim3(unsigned(groups)), dim3(64 * NW), 0, a.stream,
-                       P.seqlens, P.q, P.k_cache, P.v_cache, P.B, P.n_groups, P.window,
-                       P.lo_floor, P.T_max, P.n_units, P);
+    nt ? stream_pass(decode_fused_kernel<true>) : stream_pass(decode_fused_kernel<false>);
   int st = launch_status("decode_fused");
   if (st != MCAMD_OK) return st;
   const dim3 merge_grid(unsigned(a.batch * P.n_units * KG * GM));

@@ -81,18 +81,6 @@ constexpr int kDecodePartFloats =
 #define MCAMD_PREFIX_SPLITS 16
 #endif
 constexpr int kPrefixMaxSplits = MCAMD_PREFIX_SPLITS;
-struct PrefixArgs {
-  const void *q, *k_cache, *v_cache;
-  float *part;
-  int64_t rows, n_head, n_kv_head, t_max, cache_batch_stride, prefix;
-  int n_split;
-  hipStream_t stream;
-};
-int launch_prefix_partials(const PrefixArgs &a);
-// Key ranges for launch_prefix_partials: enough workgroups to fill `cus` compute units, at most
-// max_splits, and at least 128 keys per range.
-int prefix_partial_splits(int64_t rows, int64_t n_head, int64_t n_kv_head, int64_t prefix,
-                          int cus, int max_splits);
 // Bytes of workspace past decode_workspace_bytes() for those partials (0 where the fused decode
 // never takes the prefix on the matrix cores: such calls read row 0's keys in the streaming pass).
 size_t decode_prefix_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,

@@ -46,8 +46,8 @@
 // In the matrix phase the LDS reads of the next 16-key step are issued (as inline asm, with
 // explicit waits) before the products of the current one, so the LDS streams under the MFMAs.
 //
-// The shared prompt prefix of a decode step (launch_prefix_partials) runs in a kernel of its own
-// below, built from the same fragments and layouts.
+// The shared prompt prefix of a decode step runs inside the fused decode kernel (prefix_mfma.h),
+// built from the same fragments and layouts.
 #include "kernels.h"
 
 #include <cmath>
@@ -464,339 +464,6 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
     }
 }
 
-// Shared prompt prefix of a decode step (prefix_mfma_kernel): the queries of every row, all
-// against keys [0, prefix) of row 0. A KV head's (row, query head) pairs -- rows x G of them,
-// head fastest -- form groups of 32 (one wave's MFMA columns); a workgroup owns one pair group,
-// one KV head and one key range, and its four waves (one per SIMD) split that range in four
-// consecutive parts, each streaming its own 32-key K/V tiles (double-buffered in its own LDS,
-// filled by DMA) through the same products as the chunked prefill. The waves' (o, m, l) are
-// combined through LDS at the end, so the decode's merge pass reads one partial per key range
-// instead of one per wave. No key of the prefix is masked: every decode query sits past it.
-// Workgroup ids place the pair groups of one (KV head, range) on one XCD (ids 8 apart), where
-// they share its L2 for the K/V they all read.
-constexpr int kPxWaves = 4;
-constexpr int kPxThreads = 64 * kPxWaves;
-constexpr int kPxKT = 32;              // keys per tile
-constexpr int kPxTile = kPxKT * D;     // elements of one K (or V) tile
-constexpr int kPxMinKeys = 128;        // keys per range, at least
-
-struct PrefixParams {
-  const uint16_t *q, *k_cache, *v_cache;  // q: (rows, H, D); keys and values of cache row 0
-  float *part;
-  int H, H_kv, G, n_pairs, n_pg, n_split, key_len, prefix, n_units, n_hc, T_max;
-  float scale_log2;
-};
-
-// The leading arguments are the fields the kernel needs first, passed separately so that they
-// arrive preloaded in SGPRs instead of behind a load of the argument buffer.
-__global__ __launch_bounds__(kPxThreads, 1) void prefix_mfma_kernel(
-    const uint16_t *a_q, const uint16_t *a_k_cache, const uint16_t *a_v_cache, int a_n_pg,
-    int a_n_split, int a_key_len, int a_prefix, int a_H, int a_H_kv, PrefixParams P) {
-  P.q = a_q;
-  P.k_cache = a_k_cache;
-  P.v_cache = a_v_cache;
-  P.n_pg = a_n_pg;
-  P.n_split = a_n_split;
-  P.key_len = a_key_len;
-  P.prefix = a_prefix;
-  P.H = a_H;
-  P.H_kv = a_H_kv;
-  __shared__ __attribute__((aligned(1024))) uint16_t sK[kPxWaves][2][kPxTile];
-  __shared__ __attribute__((aligned(1024))) uint16_t sV[kPxWaves][2][kPxTile];
-  __shared__ float sM[kPxWaves][32], sL[kPxWaves][32];
-
-  // Block id -> (KV head, key range, pair group).
-  const int id = blockIdx.x;
-  const int n_ks = P.H_kv * P.n_split;
-  int ks, pg;
-  if (n_ks % 8 == 0) {
-    const int c = id >> 3;
-    ks = (id & 7) + 8 * (c / P.n_pg);
-    pg = c % P.n_pg;
-  } else {
-    ks = id / P.n_pg;
-    pg = id - ks * P.n_pg;
-  }
-  const int kvh = ks / P.n_split;
-  const int split = ks - kvh * P.n_split;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int h = lane >> 5;
-  const int col = lane & 31;
-
-  const int pr = pg * 32 + col;
-  const bool live = pr < P.n_pairs;
-  const int pp = live ? pr : P.n_pairs - 1;  // dead pairs compute on a live one
-  const int row = pp / P.G;
-  const int head = pp - row * P.G;
-
-  // Q^T fragments: B[k = dim][n = pair], lane holds pair `col`, dims 16 kd + 8 h .. + 7. Loaded
-  // as inline asm, ahead of every DMA, and used only after the first tile's wait (which then
-  // covers them): the compiler's own waits for tracked loads would stall the first tile on the
-  // second tile's DMAs as well.
-  bf16x8 qf[8];
-  {
-    const uint16_t *qp = P.q + (int64_t(row) * P.H + int64_t(kvh) * P.G + head) * D + 8 * h;
-    asm volatile(
-        "global_load_dwordx4 %0, %8, off\n"
-        "global_load_dwordx4 %1, %8, off offset:32\n"
-        "global_load_dwordx4 %2, %8, off offset:64\n"
-        "global_load_dwordx4 %3, %8, off offset:96\n"
-        "global_load_dwordx4 %4, %8, off offset:128\n"
-        "global_load_dwordx4 %5, %8, off offset:160\n"
-        "global_load_dwordx4 %6, %8, off offset:192\n"
-        "global_load_dwordx4 %7, %8, off offset:224"
-        : "=&v"(qf[0]), "=&v"(qf[1]), "=&v"(qf[2]), "=&v"(qf[3]), "=&v"(qf[4]), "=&v"(qf[5]),
-          "=&v"(qf[6]), "=&v"(qf[7])
-        : "v"(qp)
-        : "memory");
-  }
-
-  // This wave's keys: part `wave` of the workgroup's range [r_lo, r_hi).
-  const int r_lo = split * P.key_len;
-  const int r_hi = min(P.prefix, r_lo + P.key_len);
-  const int wl = (r_hi - r_lo + kPxWaves - 1) / kPxWaves;
-  const int k_lo = r_lo + wave * wl;
-  const int k_hi = min(r_hi, k_lo + wl);
-  const int n_t = k_hi > k_lo ? (k_hi - k_lo + kPxKT - 1) / kPxKT : 0;
-
-  const int64_t tok = int64_t(P.H_kv) * D;
-  const uint32_t tok_bytes = uint32_t(tok) * 2u;
-  const uint32_t extent = uint32_t(P.T_max - 1) * tok_bytes + uint32_t(D) * 2u;
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(P.k_cache + int64_t(kvh) * D), 0, int(extent), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(P.v_cache + int64_t(kvh) * D), 0, int(extent), 0x00020000);
-  const uint32_t k_lane_off = uint32_t(8 * h) * 2u;
-  const uint32_t v_chunk = uint32_t((lane & 15) ^ (4 * ((lane >> 4) & 3)));
-  uint16_t *myK = &sK[wave][0][0];
-  uint16_t *myV = &sV[wave][0][0];
-  // Tile t into buffer `buf`: eight K fragments (keys k0 + col, dims 16 f + 8 h .. + 7, in lane
-  // order) and eight blocks of four V rows (chunks swizzled); keys past k_hi re-read k_hi - 1.
-  auto issue_tile = [&](int t, int buf) {
-    const int k0 = k_lo + t * kPxKT;
-#pragma unroll
-    for (int f = 0; f < 8; ++f) {
-      const uint32_t kkey = uint32_t(min(k0 + col, k_hi - 1));
-      const uint32_t off = __umul24(kkey, tok_bytes) + uint32_t(16 * f) * 2u + k_lane_off;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rk, (__attribute__((address_space(3))) void *)(myK + buf * kPxTile + f * 512), 16,
-          int(off), 0, 0, 0);
-    }
-#pragma unroll
-    for (int f = 0; f < 8; ++f) {
-      const uint32_t vkey = uint32_t(min(k0 + 4 * f + (lane >> 4), k_hi - 1));
-      const uint32_t off = __umul24(vkey, tok_bytes) + ((v_chunk ^ uint32_t(f & 3)) << 4);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rv, (__attribute__((address_space(3))) void *)(myV + buf * kPxTile + f * 512), 16,
-          int(off), 0, 0, 0);
-    }
-  };
-
-  f32x16 o[4];
-#pragma unroll
-  for (int md = 0; md < 4; ++md)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) o[md][e] = 0.f;
-  float m = -INFINITY;
-  float l = 0.f;
-
-  const int L16 = lane & 15;
-  const int tr_row = L16 >> 2;
-  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (L16 & 3);
-  int vofs[8];  // element offsets of this lane's transpose reads for 16-key step 0
-#pragma unroll
-  for (int md = 0; md < 4; ++md) {
-    const int r0 = 4 * h + tr_row, r1 = r0 + 8;
-    const int cc = 32 * md + tr_col;
-    vofs[md] = r0 * D + (((cc >> 3) ^ swz(r0)) << 3) + (cc & 7);
-    vofs[4 + md] = r1 * D + (((cc >> 3) ^ swz(r1)) << 3) + (cc & 7);
-  }
-
-  // Tile t has landed once only the sixteen DMAs of tile t + 1 may be pending. The first wait
-  // sits before the loop: it also covers the q loads (older than every DMA), so the compiler's
-  // own waits for them stay out of the loop.
-  auto wait_tile = [&](int t) {
-    if (t + 1 < n_t)
-      __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16)
-    else
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    asm volatile("" ::: "memory");
-  };
-  if (n_t > 0) issue_tile(0, 0);
-  if (n_t > 1) issue_tile(1, 1);
-  wait_tile(0);
-  if (n_t == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (no tile: the q loads)
-  asm volatile(""
-               : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]), "+v"(qf[4]), "+v"(qf[5]),
-                 "+v"(qf[6]), "+v"(qf[7]));
-  for (int t = 0; t < n_t; ++t) {
-    const int buf = t & 1;
-    if (t > 0) wait_tile(t);
-    // LDS reads as inline asm (the compiler would otherwise order every read of the tiles
-    // after all pending DMAs, the next tile's included), each used behind an explicit wait.
-    const uint32_t ka = lds_addr(myK + buf * kPxTile + lane * 8);
-    const uint32_t vb = lds_addr(myV + buf * kPxTile);
-    bf16x8 kf[8];
-    ds_read_b128<0 * 1024>(kf[0], ka);
-    ds_read_b128<1 * 1024>(kf[1], ka);
-    ds_read_b128<2 * 1024>(kf[2], ka);
-    ds_read_b128<3 * 1024>(kf[3], ka);
-    ds_read_b128<4 * 1024>(kf[4], ka);
-    ds_read_b128<5 * 1024>(kf[5], ka);
-    ds_read_b128<6 * 1024>(kf[6], ka);
-    ds_read_b128<7 * 1024>(kf[7], ka);
-    // S^T (32 keys x 32 pairs): s[4j + i] is key k0 + 8 j + 4 h + i of pair `col`.
-    f32x16 s;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) s[e] = 0.f;
-    lgkm_wait<7>(kf[0]);
-    s = mfma(kf[0], qf[0], s);
-    lgkm_wait<6>(kf[1]);
-    s = mfma(kf[1], qf[1], s);
-    lgkm_wait<5>(kf[2]);
-    s = mfma(kf[2], qf[2], s);
-    lgkm_wait<4>(kf[3]);
-    s = mfma(kf[3], qf[3], s);
-    lgkm_wait<3>(kf[4]);
-    s = mfma(kf[4], qf[4], s);
-    lgkm_wait<2>(kf[5]);
-    s = mfma(kf[5], qf[5], s);
-    lgkm_wait<1>(kf[6]);
-    s = mfma(kf[6], qf[6], s);
-    lgkm_wait<0>(kf[7]);
-    s = mfma(kf[7], qf[7], s);
-    // The V^T fragments of both 16-key steps, read while the softmax below runs.
-    bf16x4 vf[2][4][2];
-    ds_read_tr<0>(vf[0][0][0], vb + 2 * vofs[0]);
-    ds_read_tr<0>(vf[0][0][1], vb + 2 * vofs[4]);
-    ds_read_tr<0>(vf[0][1][0], vb + 2 * vofs[1]);
-    ds_read_tr<0>(vf[0][1][1], vb + 2 * vofs[5]);
-    ds_read_tr<0>(vf[0][2][0], vb + 2 * vofs[2]);
-    ds_read_tr<0>(vf[0][2][1], vb + 2 * vofs[6]);
-    ds_read_tr<0>(vf[0][3][0], vb + 2 * vofs[3]);
-    ds_read_tr<0>(vf[0][3][1], vb + 2 * vofs[7]);
-    ds_read_tr<16 * D * 2>(vf[1][0][0], vb + 2 * vofs[0]);
-    ds_read_tr<16 * D * 2>(vf[1][0][1], vb + 2 * vofs[4]);
-    ds_read_tr<16 * D * 2>(vf[1][1][0], vb + 2 * vofs[1]);
-    ds_read_tr<16 * D * 2>(vf[1][1][1], vb + 2 * vofs[5]);
-    ds_read_tr<16 * D * 2>(vf[1][2][0], vb + 2 * vofs[2]);
-    ds_read_tr<16 * D * 2>(vf[1][2][1], vb + 2 * vofs[6]);
-    ds_read_tr<16 * D * 2>(vf[1][3][0], vb + 2 * vofs[3]);
-    ds_read_tr<16 * D * 2>(vf[1][3][1], vb + 2 * vofs[7]);
-    const int k0 = k_lo + t * kPxKT;
-    if (k0 + kPxKT > k_hi) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        if (k0 + 8 * (e >> 2) + 4 * h + (e & 3) >= k_hi) s[e] = -INFINITY;
-    }
-    // Weights against the running maximum; the tile's maximum is taken (and O rescaled) only
-    // when a pair's weights of the tile sum past 2^15, are not finite, or it has no maximum yet.
-    auto weights = [&](int step, float m_use, float &tl) {
-      f32x8 pv;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        pv[e] = __builtin_amdgcn_exp2f(fmaf(s[8 * step + e], P.scale_log2, -m_use));
-      tl += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
-      return __builtin_convertvector(pv, bf16x8);
-    };
-    float tl = 0.f;
-    const float m_try = m == -INFINITY ? 0.f : m;
-    bf16x8 pk0 = weights(0, m_try, tl), pk1 = weights(1, m_try, tl);
-    if (__builtin_amdgcn_ballot_w64(!(tl <= kTileSumLimit) || m == -INFINITY) != 0) {
-      float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-#pragma unroll
-      for (int e = 0; e < 16; ++e) m4[e & 3] = fmaxf(m4[e & 3], s[e]);
-      const float mx =
-          max_halves(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]))) * P.scale_log2;
-      const float m_new = fmaxf(m, mx);
-      const float alpha = m_new == -INFINITY ? 1.f : exp2_or_zero(m - m_new);
-      l *= alpha;
-#pragma unroll
-      for (int md = 0; md < 4; ++md)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) o[md][e] *= alpha;
-      m = m_new;
-      tl = 0.f;
-      const float m_use = m == -INFINITY ? 0.f : m;
-      pk0 = weights(0, m_use, tl);
-      pk1 = weights(1, m_use, tl);
-    }
-    l += tl;
-    // O^T += V^T . P^T over the tile's two 16-key steps, in the accumulators' key order.
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(vf[0][0][0]), "+v"(vf[0][0][1]), "+v"(vf[0][1][0]), "+v"(vf[0][1][1]),
-                   "+v"(vf[0][2][0]), "+v"(vf[0][2][1]), "+v"(vf[0][3][0]), "+v"(vf[0][3][1]),
-                   "+v"(vf[1][0][0]), "+v"(vf[1][0][1]), "+v"(vf[1][1][0]), "+v"(vf[1][1][1]),
-                   "+v"(vf[1][2][0]), "+v"(vf[1][2][1]), "+v"(vf[1][3][0]), "+v"(vf[1][3][1])::
-                     "memory");
-#pragma unroll
-    for (int step = 0; step < 2; ++step) {
-#pragma unroll
-      for (int md = 0; md < 4; ++md) {
-        const bf16x8 a = __builtin_shufflevector(vf[step][md][0], vf[step][md][1], 0, 1, 2, 3, 4,
-                                                 5, 6, 7);
-        o[md] = mfma(a, step == 0 ? pk0 : pk1, o[md]);
-      }
-    }
-    // Every read of this buffer has completed (the wait above), so the DMA of tile t + 2 may
-    // overwrite it.
-    if (t + 2 < n_t) issue_tile(t + 2, buf);
-  }
-
-  // Combine the four waves: each parks its (o, m, l) in its own (now idle) LDS tiles, then wave
-  // w sums dims 32 w .. + 31 of all four, scaled to the common maximum, and writes them.
-  const float lt = sum_halves(l);
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-  float *red = reinterpret_cast<float *>(myK);  // 16 KB: o[md][e] of lane at (md * 16 + e) * 64
-#pragma unroll
-  for (int md = 0; md < 4; ++md)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) red[(md * 16 + e) * 64 + lane] = o[md][e];
-  if (h == 0) {
-    sM[wave][col] = m;
-    sL[wave][col] = lt;
-  }
-  __syncthreads();
-  float mw[kPxWaves], M = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < kPxWaves; ++w) {
-    mw[w] = sM[w][col];
-    M = fmaxf(M, mw[w]);
-  }
-  float fw[kPxWaves], L = 0.f;
-#pragma unroll
-  for (int w = 0; w < kPxWaves; ++w) {
-    fw[w] = mw[w] == -INFINITY ? 0.f : exp2_or_zero(mw[w] - M);
-    L += fw[w] * sL[w][col];
-  }
-  float acc[16];
-#pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-#pragma unroll
-  for (int w = 0; w < kPxWaves; ++w) {
-    const float *rw = reinterpret_cast<const float *>(&sK[w][0][0]) + wave * 16 * 64;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = fmaf(fw[w], rw[e * 64 + lane], acc[e]);
-  }
-  if (!live) return;
-  // The unnormalised partial of (row, head) for this key range, in the decode unit's slot:
-  // unit (row, KV-head group, query-head group), entry (KV head, query head) within it.
-  const int unit = (kvh / kDecodeUnitKv) * P.n_hc + head / kDecodeUnitQ;
-  const int entry = (kvh % kDecodeUnitKv) * kDecodeUnitQ + head % kDecodeUnitQ;
-  float *slot =
-      P.part + ((int64_t(row) * P.n_units + unit) * P.n_split + split) * kDecodePartFloats;
-  float *po = slot + entry * D + 32 * wave + 4 * h;  // dims 32 wave + 8 j + 4 h + i
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    *reinterpret_cast<float4 *>(po + 8 * j) =
-        make_float4(acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]);
-  if (wave == 0 && h == 0)
-    *reinterpret_cast<float2 *>(slot + kDecodeUnitKv * kDecodeUnitQ * D + 2 * entry) =
-        make_float2(M, L);
-}
-
 }  // namespace
 
 bool prefill_mfma_geometry_ok(int64_t n_head, int64_t n_kv_head, int64_t t_max) {
@@ -836,44 +503,6 @@ int launch_prefill_mfma(const AttnArgs &a) {
   hipLaunchKernelGGL(prefill_mfma_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0,
                      a.stream, P);
   return launch_status("prefill_mfma");
-}
-
-int launch_prefix_partials(const PrefixArgs &a) {
-  PrefixParams P{};
-  P.q = static_cast<const uint16_t *>(a.q);
-  P.k_cache = static_cast<const uint16_t *>(a.k_cache);
-  P.v_cache = static_cast<const uint16_t *>(a.v_cache);
-  P.part = a.part;
-  P.H = int(a.n_head);
-  P.H_kv = int(a.n_kv_head);
-  P.G = int(a.n_head / a.n_kv_head);
-  P.n_pairs = int(a.rows) * P.G;
-  P.n_pg = (P.n_pairs + 31) / 32;
-  P.n_split = a.n_split;
-  P.key_len = int((a.prefix + a.n_split - 1) / a.n_split);
-  P.prefix = int(a.prefix);
-  P.n_hc = (P.G + kDecodeUnitQ - 1) / kDecodeUnitQ;
-  P.n_units = ((P.H_kv + kDecodeUnitKv - 1) / kDecodeUnitKv) * P.n_hc;
-  P.T_max = int(a.t_max);
-  P.scale_log2 = float(kLog2e / std::sqrt(double(D)));
-  // Every key range must hold keys: (n_split - 1) * ceil(prefix / n_split) < prefix.
-  if (a.n_split < 1 || int64_t(a.n_split - 1) * P.key_len >= a.prefix)
-    return fail(MCAMD_EINVAL, "prefix partials: empty key range");
-  const int64_t blocks = int64_t(P.n_pg) * P.H_kv * P.n_split;
-  if (blocks > 0x7fffffff) return fail(MCAMD_EUNSUPPORTED, "prefix partials: grid too large");
-  hipLaunchKernelGGL(prefix_mfma_kernel, dim3(unsigned(blocks)), dim3(kPxThreads), 0, a.stream,
-                     P.q, P.k_cache, P.v_cache, P.n_pg, P.n_split, P.key_len, P.prefix, P.H,
-                     P.H_kv, P);
-  return launch_status("prefix_mfma");
-}
-
-int prefix_partial_splits(int64_t rows, int64_t n_head, int64_t n_kv_head, int64_t prefix,
-                          int cus, int max_splits) {
-  const int64_t G = n_head / n_kv_head;
-  const int64_t per_split = n_kv_head * ((rows * G + 31) / 32);  // workgroups per key range
-  const int64_t want = (int64_t(cus) + per_split - 1) / per_split;
-  return int(std::max<int64_t>(1, std::min<int64_t>({want, int64_t(max_splits),
-                                                      prefix / kPxMinKeys})));
 }
 
 }  // namespace mcamd
