@@ -488,9 +488,9 @@ def bench_prefill(args):
     # bytes a pass must move at least: every key read once per (row, KV head), not once per query
     # tile), against what the counters measured.
     pf_bytes = prefill_pass_bytes()
-    t, src = profile_traffic("prefill", pf_bytes)
+    t, t_src = profile_traffic("prefill", pf_bytes)
     result["roofline"].update({"traffic": t, "traffic_unit": "bytes per pass",
-                               "traffic_min_bytes": pf_bytes, "traffic_source": src})
+                               "traffic_min_bytes": pf_bytes, "traffic_source": t_src})
     if not args.no_cpu_baseline:
         log("CPU baseline: the whole chunked prefill on host cores")
         result["cpu_baseline"] = cpu_prefill_baseline(q, k, v)
@@ -575,9 +575,9 @@ def bench_replicate(args):
                      "peak": hbm_peak / 1e9, "peak_source": peak_src, "unit": "GB/s",
                      "frac": round(gbps * 1e9 / hbm_peak, 4), "bytes_per_launch": nbytes},
     }
-    t, src = profile_traffic("replicate", nbytes)
+    t, t_src = profile_traffic("replicate", nbytes)
     result["roofline"].update({"traffic": t, "traffic_unit": "bytes per launch",
-                               "traffic_source": src})
+                               "traffic_source": t_src})
     if not args.no_cpu_baseline:
         log("CPU baseline: the replication's broadcast copy on host cores")
         result["cpu_baseline"] = cpu_replicate_baseline(src)
@@ -703,9 +703,9 @@ def bench_mixed(args):
                      "frac": round(gbps * 1e9 / hbm_peak, 4),
                      "bytes_per_step": int(step_bytes)},
     }
-    t, src = profile_traffic("mixed", int(step_bytes))
+    t, t_src = profile_traffic("mixed", int(step_bytes))
     result["roofline"].update({"traffic": t, "traffic_unit": "bytes per step",
-                               "traffic_source": src})
+                               "traffic_source": t_src})
     if not args.no_cpu_baseline:
         log("CPU baseline: whole steps of the stack (24 calls) on host cores")
         result["cpu_baseline"] = cpu_mixed_baseline(cache, qs, ks, vs, windows, W)
@@ -940,19 +940,20 @@ def bench_sample(args):
 
 # The other workloads the default run measures beside the headline: (passes or steps timed,
 # untimed warm-up) each, fixed so that the run's length does not depend on --steps.
-SUBSYSTEM_STEPS = {"prefill": (3, 1), "mixed": (64, 8), "replicate": (10, 2)}
+SUBSYSTEM_STEPS = {"prefill": (3, 1), "mixed": (64, 8), "replicate": (10, 2), "sample": (492, 20)}
 SUBSYSTEM_KEEP = ("metric", "value", "unit", "ms_per_step", "steps", "warmup", "config",
                   "roofline", "append", "cpu_baseline")
 
 
 def subsystems(args):
     """The chunked prefill (attention MFMA utilisation and append GB/s), the mixed-window stack's
-    decode step and the replication of a prompt cache, each as its own object with its roofline
-    and a CPU baseline timed on the same work."""
+    decode step, the replication of a prompt cache and the large-batch sampling decode, each as
+    its own object with its roofline and a CPU baseline (timed on the same work; the sampling
+    one on a 1-layer copy of its model, labelled extrapolated)."""
     import torch
     out = {}
     for name, fn in (("prefill", bench_prefill), ("mixed", bench_mixed),
-                     ("replicate", bench_replicate)):
+                     ("replicate", bench_replicate), ("sample", bench_sample)):
         steps, warmup = SUBSYSTEM_STEPS[name]
         sub = argparse.Namespace(**{**vars(args), "steps": steps, "warmup": warmup,
                                     "workload": name})
