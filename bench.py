@@ -113,6 +113,11 @@ def parse_args():
                          "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of it (its last UNITS "
                          "passes, steps or launches, ALGO_BYTES algorithmic bytes each) and of "
                          "bench.py --calibrate-copy")
+    ap.add_argument("--summarize-pmc", nargs="+", metavar="CSV",
+                    help="print per-dispatch counter means from rocprofv3 --pmc CSVs over the "
+                         "last --launches dispatches of the kernel named by --kernel")
+    ap.add_argument("--kernel", default="prefill_mfma_kernel",
+                    help="kernel name (substring) for --summarize-pmc")
     ap.add_argument("--summarize-trace", metavar="CSV",
                     help="print the mean duration of the decode call's kernels over the last "
                          "--launches dispatches of a rocprofv3 kernel_trace.csv")
@@ -336,6 +341,21 @@ def summarize_counters(name, fetch_csv, write_csv, copy_fetch_csv, copy_write_cs
           f"bytes ({per_unit / algo_bytes:.3f}x).\n")
     print(f"traffic_bytes_per_unit: {round(per_unit)}")
     print(f"algorithmic_bytes_per_unit: {algo_bytes}")
+
+
+def summarize_pmc(csvs, kernel, last):
+    """Per-dispatch means of every counter in rocprofv3 --pmc runs (one CSV per pass) over the
+    last `last` dispatches of the kernels whose name contains `kernel`."""
+    import collections
+    per = collections.defaultdict(dict)  # counter -> dispatch -> value
+    for path in csvs:
+        for r in _counter_rows(path):
+            if kernel in r["Kernel_Name"]:
+                per[r["Counter_Name"]][int(r["Dispatch_Id"])] = float(r["Counter_Value"])
+    print(f"| counter | mean per dispatch (last {last} of `{kernel}`) |\n|---|---|")
+    for name in sorted(per):
+        vals = [per[name][d] for d in sorted(per[name])][-last:]
+        print(f"| {name} | {sum(vals) / len(vals):.6g} |")
 
 
 def prefill_pass_bytes():
@@ -996,6 +1016,9 @@ def main():
         return
     if args.summarize_trace:
         summarize_trace(args.summarize_trace, args.launches)
+        return
+    if args.summarize_pmc:
+        summarize_pmc(args.summarize_pmc, args.kernel, args.launches)
         return
     if args.summarize_counters:
         name, f, w, cf, cw, units, algo = args.summarize_counters
