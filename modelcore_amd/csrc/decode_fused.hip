@@ -924,7 +924,7 @@ int launch_decode_fused(const AttnArgs &a) {
     X.H_kv = P.H_kv;
     X.G = P.G;
     X.n_pairs = P.B * P.G;
-    X.n_pg = (X.n_pairs + 31) / 32;
+    X.n_pb = (X.n_pairs + px::kPairsPerJob - 1) / px::kPairsPerJob;
     X.n_split = P.n_pre;
     X.key_len = int((a.shared_prefix + P.n_pre - 1) / P.n_pre);
     X.prefix = int(a.shared_prefix);
@@ -932,7 +932,7 @@ int launch_decode_fused(const AttnArgs &a) {
     X.n_hc = P.n_hc;
     X.T_max = P.T_max;
     X.scale_log2 = P.scale_log2;
-    X.jobs = X.n_pg * P.H_kv * P.n_pre;
+    X.jobs = X.n_pb * P.H_kv * P.n_pre;
     // Every key range holds keys: (n_pre - 1) * ceil(prefix / n_pre) < prefix, since at most
     // sixteen ranges of at least 128 keys are made.
     if (int64_t(P.n_pre - 1) * X.key_len >= a.shared_prefix)
@@ -976,8 +976,10 @@ int launch_decode_fused(const AttnArgs &a) {
   };
   constexpr int S16 = kSpec < 16 ? kSpec : 16, S8 = kSpec < 8 ? kSpec : 8,
                 S4 = kSpec < 4 ? kSpec : 4;
-  if (P.n_pre > 4)
+  if (P.n_pre > 8)
     merge(decode_merge_kernel<S4, kPrefixMaxSplits>);
+  else if (P.n_pre > 4)
+    merge(decode_merge_kernel<S4, 8>);
   else if (P.n_pre > 0)
     merge(decode_merge_kernel<S4, 4>);
   else if (kSpec >= 16 && per_unit > 8)

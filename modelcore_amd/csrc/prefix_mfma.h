@@ -7,28 +7,30 @@
 // query head), which the decode's merge pass combines with the row's own keys by log-sum-exp.
 //
 // Work split. A KV head's (row, query head) pairs -- rows x G of them, head fastest -- form
-// groups of 32 (one wave's MFMA columns); a job owns one pair group, one KV head and one key
-// range, and the workgroup's four waves (one per SIMD) split that range in four consecutive
-// parts, each streaming its own 32-key tiles -- K straight into registers, V through its own
-// double-buffered LDS, filled by DMA -- through v_mfma_f32_32x32x16_bf16:
-//   S^T (keys x pairs) = K (keys x D) . Q^T (D x pairs)       A = K, B = Q, both in registers
+// blocks of 64; a job owns one block, one KV head and one key range. Its four waves (one per
+// SIMD) are two pair groups of 32 (one wave's MFMA columns) times two halves of the range: the
+// two waves of a half share that half's 32-key K and V tiles, double-buffered in LDS and filled
+// by DMA, and run them through v_mfma_f32_32x32x16_bf16:
+//   S^T (keys x pairs) = K (keys x D) . Q^T (D x pairs)       A = K from LDS, B = Q in registers
 //   O^T (D x pairs)   += V^T (D x keys) . P^T (keys x pairs)   A = V^T via ds_read_b64_tr_b16
 // The transposed scores come out with one pair per lane (lane l: pair l % 32, keys 8 j + 4 (l /
 // 32) + i), the layout the second product wants for its B operand; the 16 keys of a step are
 // taken in that order, and the V^T fragment reads the same keys (two transpose reads of four
 // rows). Online softmax per pair in fp32 (exp2 domain), the tile's maximum taken only when a
 // pair's weights of the tile sum past 2^15, are not finite, or it has no maximum yet. No key of
-// the prefix is masked: every decode query sits past it. The four waves' (o, m, l) are combined
-// through LDS at the end, so the merge reads one partial per key range. Job ids place the pair
-// groups of one (KV head, range) on one XCD (ids 8 apart), where they share its L2.
+// the prefix is masked: every decode query sits past it. The two halves' (o, m, l) of a pair
+// group are combined through LDS at the end, so the merge reads one partial per key range. Job
+// ids place the pair blocks of one (KV head, range) on one XCD (ids 8 apart), where they share
+// its L2.
 //
-// The products' k index (the head dim) runs in any order common to both operands of S: fragment
-// kd of lane half h holds dims 64 h + 8 kd .. + 7, so a lane's K of a tile is 128 contiguous
-// bytes of its key's row (eight 16-byte loads) and its q likewise.
-// V in LDS (per wave and buffer, 8 KiB): rows in natural order, 16-byte chunk c of row r at slot
-// c ^ swz(r), under which the transpose reads (four consecutive rows, 32 bytes each per 16 lanes)
-// use every bank. A job's LDS (65 KiB) and registers (at most 256) leave room for a streaming
-// workgroup of the decode beside it on every compute unit.
+// LDS layouts (per key half and buffer, 8 KiB each of K and V):
+//  * K fragment-major: block kd (dims 16 kd .. + 15) holds the A fragment of the tile's 32 keys
+//    in lane order, so a wave reads a fragment as one contiguous 1 KiB.
+//  * V rows in natural order, 16-byte chunk c of row r at slot c ^ swz(r), under which the
+//    transpose reads (four consecutive rows, 32 bytes each per 16 lanes) use every bank.
+// A job's LDS (65 KiB) and registers (at most 256) leave room for a streaming workgroup of the
+// decode beside it on every compute unit; the two share that CU's load path, so a job loads each
+// K/V tile once for 64 pairs (half the bytes of one wave per 32 pairs).
 #pragma once
 
 #include <type_traits>
@@ -44,10 +46,12 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kKT = 32;              // keys per tile
 constexpr int kTile = kKT * kD;      // elements of one K (or V) tile
 constexpr int kMinKeys = 128;        // keys per range, at least
+constexpr int kPairsPerJob = 64;     // (row, query head) pairs of one KV head per job
 constexpr float kTileSumLimit = 32768.f;  // 2^15: a pair's weights of one tile sum to at most this
-// LDS of a job: V tiles (two buffers per wave; the waves' o at the end), then their (m, l).
-constexpr int kVBytes = kWaves * 2 * kTile * 2;
-constexpr int kLdsBytes = kVBytes + 2 * kWaves * 32 * 4;
+// LDS of a job: two key halves x two buffers x (K tile + V tile), 64 KiB (the waves' o at the
+// end), then the waves' (m, l).
+constexpr int kTileBytes = 2 * 2 * 2 * kTile * 2;
+constexpr int kLdsBytes = kTileBytes + 2 * kWaves * 32 * 4;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -57,7 +61,7 @@ typedef float f32x8 __attribute__((ext_vector_type(8)));
 struct Params {
   const uint16_t *q, *k_cache, *v_cache;  // q: (rows, H, D); keys and values of cache row 0
   float *part;  // slot ((row * n_units + unit) * n_split + range) of kDecodePartFloats floats
-  int H, H_kv, G, n_pairs, n_pg, n_split, key_len, prefix, n_units, n_hc, T_max, jobs;
+  int H, H_kv, G, n_pairs, n_pb, n_split, key_len, prefix, n_units, n_hc, T_max, jobs;
   float scale_log2;
 };
 
@@ -66,7 +70,7 @@ struct Params {
 inline int splits(int64_t rows, int64_t n_head, int64_t n_kv_head, int64_t prefix, int cus,
                   int max_splits) {
   const int64_t G = n_head / n_kv_head;
-  const int64_t per_split = n_kv_head * ((rows * G + 31) / 32);  // jobs per key range
+  const int64_t per_split = n_kv_head * ((rows * G + kPairsPerJob - 1) / kPairsPerJob);
   const int64_t want = (int64_t(cus) + per_split - 1) / per_split;
   int64_t n = want < max_splits ? want : max_splits;
   if (n > prefix / kMinKeys) n = prefix / kMinKeys;
@@ -85,8 +89,16 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // would order every read of a tile after all of them, the next tile's included). Every result is
 // used only behind an explicit `s_waitcnt lgkmcnt` that takes it as an operand.
 template <int OFF>
+__device__ __forceinline__ void ds_read_b128(bf16x8 &d, uint32_t addr) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "i"(OFF));
+}
+template <int OFF>
 __device__ __forceinline__ void ds_read_tr(bf16x4 &d, uint32_t addr) {
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "i"(OFF));
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait(bf16x8 &r) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(r) : "i"(N));
 }
 // Across the two 32-lane halves of the wave (lane l with lane l ^ 32).
 __device__ __forceinline__ float max_halves(float x) {
@@ -106,64 +118,69 @@ __device__ __forceinline__ float exp2_or_zero(float x) {
 // Job `id` (< P.jobs) of the prefix, run by all kThreads threads of the workgroup with `lds`
 // pointing to kLdsBytes of shared memory (1 KiB aligned).
 __device__ __forceinline__ void job(const Params &P, int id, unsigned char *lds) {
-  // Job id -> (KV head, key range, pair group).
+  // Job id -> (KV head, key range, block of kPairsPerJob pairs).
   const int n_ks = P.H_kv * P.n_split;
-  int ks, pg;
+  int ks, pb;
   if (n_ks % 8 == 0) {
     const int c = id >> 3;
-    ks = (id & 7) + 8 * (c / P.n_pg);
-    pg = c % P.n_pg;
+    ks = (id & 7) + 8 * (c / P.n_pb);
+    pb = c % P.n_pb;
   } else {
-    ks = id / P.n_pg;
-    pg = id - ks * P.n_pg;
+    ks = id / P.n_pb;
+    pb = id - ks * P.n_pb;
   }
   const int kvh = ks / P.n_split;
   const int split = ks - kvh * P.n_split;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave & 1;   // this wave's 32 pairs: the block's first or second
+  const int half = wave >> 1; // this wave's half of the key range
   const int h = lane >> 5;
   const int col = lane & 31;
-  uint16_t *myV = reinterpret_cast<uint16_t *>(lds) + wave * 2 * kTile;
-  float *sM = reinterpret_cast<float *>(lds + kVBytes);  // [kWaves][32]
+  // LDS: per key half, two buffers of one K tile (fragment-major) and one V tile (swizzled);
+  // the two waves of a half (one per pair group) share them.
+  uint16_t *sK = reinterpret_cast<uint16_t *>(lds) + half * 2 * kTile;
+  uint16_t *sV = reinterpret_cast<uint16_t *>(lds) + (4 + half * 2) * kTile;
+  float *sM = reinterpret_cast<float *>(lds + kTileBytes);  // [kWaves][32]
   float *sL = sM + kWaves * 32;
 
-  const int pr = pg * 32 + col;
+  const int pr = pb * kPairsPerJob + grp * 32 + col;
   const bool live = pr < P.n_pairs;
   const int pp = live ? pr : P.n_pairs - 1;  // dead pairs compute on a live one
   const int row = pp / P.G;
   const int head = pp - row * P.G;
 
-  // Q^T fragments: B[k = dim][n = pair], lane holds pair `col`, dims 64 h + 8 kd .. + 7. Loaded
-  // as inline asm, ahead of every other load, and used only after the first tile's wait (which
-  // then covers them): the compiler's own waits for tracked loads would also stall the first
-  // tile on the second tile's DMAs.
+  // Q^T fragments: B[k = dim][n = pair], lane holds pair `col`, dims 16 kd + 8 h .. + 7. Loaded
+  // as inline asm, ahead of every DMA, and used only after the first tile's wait (which then
+  // covers them): the compiler's own waits for tracked loads would also wait for DMAs.
   bf16x8 qf[8];
   {
-    const uint16_t *qp = P.q + (int64_t(row) * P.H + int64_t(kvh) * P.G + head) * kD + 64 * h;
+    const uint16_t *qp = P.q + (int64_t(row) * P.H + int64_t(kvh) * P.G + head) * kD + 8 * h;
     asm volatile(
         "global_load_dwordx4 %0, %8, off\n"
-        "global_load_dwordx4 %1, %8, off offset:16\n"
-        "global_load_dwordx4 %2, %8, off offset:32\n"
-        "global_load_dwordx4 %3, %8, off offset:48\n"
-        "global_load_dwordx4 %4, %8, off offset:64\n"
-        "global_load_dwordx4 %5, %8, off offset:80\n"
-        "global_load_dwordx4 %6, %8, off offset:96\n"
-        "global_load_dwordx4 %7, %8, off offset:112"
+        "global_load_dwordx4 %1, %8, off offset:32\n"
+        "global_load_dwordx4 %2, %8, off offset:64\n"
+        "global_load_dwordx4 %3, %8, off offset:96\n"
+        "global_load_dwordx4 %4, %8, off offset:128\n"
+        "global_load_dwordx4 %5, %8, off offset:160\n"
+        "global_load_dwordx4 %6, %8, off offset:192\n"
+        "global_load_dwordx4 %7, %8, off offset:224"
         : "=&v"(qf[0]), "=&v"(qf[1]), "=&v"(qf[2]), "=&v"(qf[3]), "=&v"(qf[4]), "=&v"(qf[5]),
           "=&v"(qf[6]), "=&v"(qf[7])
         : "v"(qp)
         : "memory");
   }
 
-  // This wave's keys: part `wave` of the job's range [r_lo, r_hi) (never empty: at least
-  // kMinKeys keys per range).
+  // This wave's keys: half `half` of the job's range [r_lo, r_hi) (at least kMinKeys keys, so
+  // both halves hold keys). Both halves take the same number of tiles (the barriers are the
+  // workgroup's); keys past k_hi are masked.
   const int r_lo = split * P.key_len;
   const int r_hi = min(P.prefix, r_lo + P.key_len);
-  const int wl = (r_hi - r_lo + kWaves - 1) / kWaves;
-  const int k_lo = r_lo + wave * wl;
-  const int k_hi = min(r_hi, k_lo + wl);
-  const int n_t = k_hi > k_lo ? (k_hi - k_lo + kKT - 1) / kKT : 0;
+  const int hl = (r_hi - r_lo + 1) / 2;
+  const int k_lo = r_lo + half * hl;
+  const int k_hi = min(r_hi, k_lo + hl);
+  const int n_t = (hl + kKT - 1) / kKT;
 
   // K/V of row 0's KV head as buffer resources: 32-bit byte offsets from the head's first
   // element, bounded by the last key of the cache.
@@ -173,39 +190,31 @@ __device__ __forceinline__ void job(const Params &P, int id, unsigned char *lds)
       (void *)(P.k_cache + int64_t(kvh) * kD), 0, int(extent), 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
       (void *)(P.v_cache + int64_t(kvh) * kD), 0, int(extent), 0x00020000);
+  const uint32_t k_lane_off = uint32_t(8 * h) * 2u;
   const uint32_t v_chunk = uint32_t((lane & 15) ^ (4 * ((lane >> 4) & 3)));
-  // K of tile t into registers: fragment f of lane (key k0 + col, half h) = dims 64 h + 8 f ..
-  // + 7 (keys past k_hi re-read k_hi - 1). Inline asm, like the q loads: the compiler counts
-  // only its own loads, not the DMAs between them, and would wait for those too.
-  const uint16_t *kbase = P.k_cache + int64_t(kvh) * kD + 64 * h;
-  auto load_k = [&](bf16x8 (&kf)[8], int t) {
-    const int key = min(k_lo + t * kKT + col, k_hi - 1);
-    const uint16_t *kp = kbase + int64_t(key) * P.H_kv * kD;
-    asm volatile(
-        "global_load_dwordx4 %0, %8, off\n"
-        "global_load_dwordx4 %1, %8, off offset:16\n"
-        "global_load_dwordx4 %2, %8, off offset:32\n"
-        "global_load_dwordx4 %3, %8, off offset:48\n"
-        "global_load_dwordx4 %4, %8, off offset:64\n"
-        "global_load_dwordx4 %5, %8, off offset:80\n"
-        "global_load_dwordx4 %6, %8, off offset:96\n"
-        "global_load_dwordx4 %7, %8, off offset:112"
-        : "=&v"(kf[0]), "=&v"(kf[1]), "=&v"(kf[2]), "=&v"(kf[3]), "=&v"(kf[4]), "=&v"(kf[5]),
-          "=&v"(kf[6]), "=&v"(kf[7])
-        : "v"(kp)
-        : "memory");
-  };
-  // V of tile t into buffer `buf`: eight blocks of four rows (chunks swizzled); keys past k_hi
-  // re-read k_hi - 1.
-  auto issue_v = [&](int t, int buf) {
+  // Tile t of this half into buffer t % 2: sixteen DMAs of 1 KiB, the half's wave of pair group
+  // g issuing K fragments 4 g .. + 3 (keys k0 + col, dims 16 f + 8 h .. + 7, in lane order) and
+  // V blocks 4 g .. + 3 (four rows, chunks swizzled); keys past k_hi re-read k_hi - 1.
+  auto issue_tile = [&](int t) {
     const int k0 = k_lo + t * kKT;
+    const int buf = t & 1;
 #pragma unroll
-    for (int f = 0; f < 8; ++f) {
-      const uint32_t vkey = uint32_t(min(k0 + 4 * f + (lane >> 4), k_hi - 1));
-      const uint32_t off = __umul24(vkey, tok_bytes) + ((v_chunk ^ uint32_t(f & 3)) << 4);
+    for (int i = 0; i < 4; ++i) {
+      const int f = 4 * grp + i;
+      const uint32_t kkey = uint32_t(min(k0 + col, k_hi - 1));
+      const uint32_t koff = __umul24(kkey, tok_bytes) + uint32_t(16 * f) * 2u + k_lane_off;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rv, (__attribute__((address_space(3))) void *)(myV + buf * kTile + f * 512), 16,
-          int(off), 0, 0, 0);
+          rk, (__attribute__((address_space(3))) void *)(sK + buf * kTile + f * 512), 16,
+          int(koff), 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f = 4 * grp + i;
+      const uint32_t vkey = uint32_t(min(k0 + 4 * f + (lane >> 4), k_hi - 1));
+      const uint32_t voff = __umul24(vkey, tok_bytes) + ((v_chunk ^ uint32_t(f & 3)) << 4);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rv, (__attribute__((address_space(3))) void *)(sV + buf * kTile + f * 512), 16,
+          int(voff), 0, 0, 0);
     }
   };
 
@@ -229,40 +238,50 @@ __device__ __forceinline__ void job(const Params &P, int id, unsigned char *lds)
     vofs[4 + md] = 2 * (r1 * kD + (((cc >> 3) ^ swz(r1)) << 3) + (cc & 7));
   }
 
-  // K one tile ahead in registers, V two tiles ahead in the LDS buffers. Load order: q, V(0),
-  // K(0), V(1), then per tile t: K(t + 1) after the scores of t, V(t + 2) after its products.
-  // At the top of tile t, K(t) and V(t) have landed once only the eight DMAs of V(t + 1) may be
-  // pending (none when t is the last tile). The first wait also covers the q loads.
-  auto wait_tile = [&](int t) {
-    if (t + 1 < n_t)
-      __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
-    else
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    asm volatile("" ::: "memory");
-  };
-  bf16x8 kf[8];
-  if (n_t > 0) {
-    issue_v(0, 0);
-    load_k(kf, 0);
-  }
-  if (n_t > 1) issue_v(1, 1);
-  if (n_t == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (no tile: the q loads)
+  // One tile ahead. At the top of tile t, this wave's DMAs of tile t are its only ones pending
+  // (the first wait also covers the q loads); the barrier then makes both waves' DMAs of the
+  // half's tile t visible, and both have finished tile t - 1, whose buffer tile t + 1 then takes.
+  // A bare barrier: a fence, even one for LDS alone, would wait for every DMA in flight.
+  issue_tile(0);
   for (int t = 0; t < n_t; ++t) {
-    const int buf = t & 1;
-    wait_tile(t);
-    // The registers the loads wrote are read only from here on.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    if (t + 1 < n_t) issue_tile(t + 1);
     asm volatile(""
                  : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]), "+v"(qf[4]), "+v"(qf[5]),
-                   "+v"(qf[6]), "+v"(qf[7]), "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3]),
-                   "+v"(kf[4]), "+v"(kf[5]), "+v"(kf[6]), "+v"(kf[7]));
-    const uint32_t vb = lds_addr(myV + buf * kTile);
+                   "+v"(qf[6]), "+v"(qf[7]));
+    const int buf = t & 1;
+    const uint32_t ka = lds_addr(sK + buf * kTile + lane * 8);
+    const uint32_t vb = lds_addr(sV + buf * kTile);
+    bf16x8 kf[8];
+    ds_read_b128<0 * 1024>(kf[0], ka);
+    ds_read_b128<1 * 1024>(kf[1], ka);
+    ds_read_b128<2 * 1024>(kf[2], ka);
+    ds_read_b128<3 * 1024>(kf[3], ka);
+    ds_read_b128<4 * 1024>(kf[4], ka);
+    ds_read_b128<5 * 1024>(kf[5], ka);
+    ds_read_b128<6 * 1024>(kf[6], ka);
+    ds_read_b128<7 * 1024>(kf[7], ka);
     // S^T (32 keys x 32 pairs): s[4j + i] is key k0 + 8 j + 4 h + i of pair `col`.
     f32x16 s;
 #pragma unroll
     for (int e = 0; e < 16; ++e) s[e] = 0.f;
-#pragma unroll
-    for (int kd = 0; kd < 8; ++kd) s = mfma(kf[kd], qf[kd], s);
-    if (t + 1 < n_t) load_k(kf, t + 1);
+    lgkm_wait<7>(kf[0]);
+    s = mfma(kf[0], qf[0], s);
+    lgkm_wait<6>(kf[1]);
+    s = mfma(kf[1], qf[1], s);
+    lgkm_wait<5>(kf[2]);
+    s = mfma(kf[2], qf[2], s);
+    lgkm_wait<4>(kf[3]);
+    s = mfma(kf[3], qf[3], s);
+    lgkm_wait<3>(kf[4]);
+    s = mfma(kf[4], qf[4], s);
+    lgkm_wait<2>(kf[5]);
+    s = mfma(kf[5], qf[5], s);
+    lgkm_wait<1>(kf[6]);
+    s = mfma(kf[6], qf[6], s);
+    lgkm_wait<0>(kf[7]);
+    s = mfma(kf[7], qf[7], s);
     // The V^T fragments of the first 16-key step, read while the softmax below runs (those of
     // the second step after it, while the first step's products run).
     bf16x4 vf[2][4][2];
@@ -338,16 +357,15 @@ __device__ __forceinline__ void job(const Params &P, int id, unsigned char *lds)
     for (int md = 0; md < 4; ++md)
       o[md] = mfma(__builtin_shufflevector(vf[1][md][0], vf[1][md][1], 0, 1, 2, 3, 4, 5, 6, 7),
                    pk1, o[md]);
-    // Every read of this buffer has completed (the wait above), so the DMA of tile t + 2 may
-    // overwrite it.
-    if (t + 2 < n_t) issue_v(t + 2, buf);
   }
 
-  // Combine the four waves: each parks its (o, m, l) in its own (now idle) V tiles, then wave w
-  // sums dims 32 w .. + 31 of all four, scaled to the common maximum, and writes them.
+  // Combine the two halves of each pair group: every wave parks its (o, m, l) (after a barrier:
+  // its partner may still read the tiles), then the wave of half x sums dims 64 x .. + 63 of
+  // both, scaled to the common maximum, and writes them.
   const float lt = sum_halves(l);
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-  float *red = reinterpret_cast<float *>(myV);  // 16 KiB: o[md][e] of lane at (md * 16 + e) * 64
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  float *red = reinterpret_cast<float *>(lds) + wave * 4096;  // o[md][e] of lane at (md*16+e)*64
 #pragma unroll
   for (int md = 0; md < 4; ++md)
 #pragma unroll
@@ -357,43 +375,39 @@ __device__ __forceinline__ void job(const Params &P, int id, unsigned char *lds)
     sL[wave * 32 + col] = lt;
   }
   __syncthreads();
-  float mw[kWaves], M = -INFINITY;
+  const int w0 = grp, w1 = grp + 2;  // the group's waves of halves 0 and 1
+  const float m0 = sM[w0 * 32 + col], m1 = sM[w1 * 32 + col];
+  const float M = fmaxf(m0, m1);
+  const float f0 = m0 == -INFINITY ? 0.f : exp2_or_zero(m0 - M);
+  const float f1 = m1 == -INFINITY ? 0.f : exp2_or_zero(m1 - M);
+  const float L = f0 * sL[w0 * 32 + col] + f1 * sL[w1 * 32 + col];
+  const float *r0 = reinterpret_cast<const float *>(lds) + w0 * 4096;
+  const float *r1 = reinterpret_cast<const float *>(lds) + w1 * 4096;
+  if (!live) return;
+  // The unnormalised partial of (row, head) for this key range, in the decode unit's slot: unit
+  // (row, KV-head group, query-head group), entry (KV head, query head) within it.
+  const int unit = (kvh / kDecodeUnitKv) * P.n_hc + head / kDecodeUnitQ;
+  const int entry = (kvh % kDecodeUnitKv) * kDecodeUnitQ + head % kDecodeUnitQ;
+  float *slot =
+      P.part + ((int64_t(row) * P.n_units + unit) * P.n_split + split) * kDecodePartFloats;
+  float *po = slot + entry * kD + 4 * h;  // o[md][4 j + i] is dim 32 md + 8 j + 4 h + i
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    mw[w] = sM[w * 32 + col];
-    M = fmaxf(M, mw[w]);
+  for (int mm = 0; mm < 2; ++mm) {
+    const int md = 2 * half + mm;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float a[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int idx = (md * 16 + 4 * j + i) * 64 + lane;
+        a[i] = fmaf(f0, r0[idx], f1 * r1[idx]);
+      }
+      *reinterpret_cast<float4 *>(po + 32 * md + 8 * j) = make_float4(a[0], a[1], a[2], a[3]);
+    }
   }
-  float fw[kWaves], L = 0.f;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    fw[w] = mw[w] == -INFINITY ? 0.f : exp2_or_zero(mw[w] - M);
-    L += fw[w] * sL[w * 32 + col];
-  }
-  float acc[16];
-#pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const float *rw = reinterpret_cast<const float *>(lds) + w * 2 * kTile / 2 + wave * 16 * 64;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = fmaf(fw[w], rw[e * 64 + lane], acc[e]);
-  }
-  if (live) {
-    // The unnormalised partial of (row, head) for this key range, in the decode unit's slot:
-    // unit (row, KV-head group, query-head group), entry (KV head, query head) within it.
-    const int unit = (kvh / kDecodeUnitKv) * P.n_hc + head / kDecodeUnitQ;
-    const int entry = (kvh % kDecodeUnitKv) * kDecodeUnitQ + head % kDecodeUnitQ;
-    float *slot =
-        P.part + ((int64_t(row) * P.n_units + unit) * P.n_split + split) * kDecodePartFloats;
-    float *po = slot + entry * kD + 32 * wave + 4 * h;  // dims 32 wave + 8 j + 4 h + i
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<float4 *>(po + 8 * j) =
-          make_float4(acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]);
-    if (wave == 0 && h == 0)
-      *reinterpret_cast<float2 *>(slot + kDecodeUnitKv * kDecodeUnitQ * kD + 2 * entry) =
-          make_float2(M, L);
-  }
+  if (half == 0 && h == 0)
+    *reinterpret_cast<float2 *>(slot + kDecodeUnitKv * kDecodeUnitQ * kD + 2 * entry) =
+        make_float2(M, L);
 }
 
 }  // namespace px
