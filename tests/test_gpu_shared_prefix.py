@@ -52,11 +52,14 @@ def _rows(n, lo, hi, seed):
 
 PREFIX_CASES = [
     # dtype, P, seqlens (all >= P), H, H_kv, D, T_max: the prefix on the matrix cores (key
-    # ranges of at least 128 keys, at most sixteen)
-    (torch.bfloat16, 2048, [2048] + _rows(63, 2048, 2560, 1), 32, 8, 128, 2560),
+    # ranges of at least 128 keys, at most sixteen, as many as fill the chip with jobs of 64
+    # (row, query head) pairs; the merge folds in 4, 8 or 16 partial slots per unit)
+    (torch.bfloat16, 2048, [2048] + _rows(63, 2048, 2560, 1), 32, 8, 128, 2560),  # 8 ranges
     (torch.bfloat16, 600, _rows(32, 600, 900, 2), 12, 4, 128, 1000),       # G = 3, 4 ranges
-    (torch.bfloat16, 1000, _rows(100, 1000, 1100, 3), 16, 4, 128, 1200),   # 400 pairs: 2 tiles
+    (torch.bfloat16, 1000, _rows(100, 1000, 1100, 3), 16, 4, 128, 1200),   # 400 pairs, 7 ranges
     (torch.bfloat16, 777, _rows(40, 777, 800, 4), 64, 8, 128, 900),        # G = 8, 6 ranges
+    (torch.bfloat16, 2100, _rows(8, 2100, 2300, 7), 16, 2, 128, 2400),     # 16 ranges, one pair block
+    (torch.bfloat16, 1301, _rows(24, 1301, 1400, 8), 24, 8, 128, 1500),    # G = 3, 72 pairs: a ragged block
 ]
 
 READ_CASES = [
