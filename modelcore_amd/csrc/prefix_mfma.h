@@ -33,8 +33,6 @@
 // K/V tile once for 64 pairs (half the bytes of one wave per 32 pairs).
 #pragma once
 
-#include <type_traits>
-
 #include "kernels.h"
 
 namespace mcamd {
