@@ -23,11 +23,11 @@
 // ids place the pair blocks of one (KV head, range) on one XCD (ids 8 apart), where they share
 // its L2.
 //
-// LDS layouts (per key half and buffer, 8 KiB each of K and V):
-//  * K fragment-major: block kd (dims 16 kd .. + 15) holds the A fragment of the tile's 32 keys
-//    in lane order, so a wave reads a fragment as one contiguous 1 KiB.
-//  * V rows in natural order, 16-byte chunk c of row r at slot c ^ swz(r), under which the
-//    transpose reads (four consecutive rows, 32 bytes each per 16 lanes) use every bank.
+// LDS layout (per key half and buffer, 8 KiB each of K and V): the tile's rows in natural order,
+// 16-byte chunk c of row r at slot c ^ swz(r). Each DMA then reads four whole rows (1 KiB
+// contiguous: eight full cache lines), and both kinds of fragment read use every bank: a K
+// fragment (sixteen consecutive rows per sixteen lanes, one chunk each) and a V^T transpose read
+// (four consecutive rows, 32 bytes each per 16 lanes).
 // A job's LDS (65 KiB) and registers (at most 256) leave room for a streaming workgroup of the
 // decode beside it on every compute unit; the two share that CU's load path, so a job loads each
 // K/V tile once for 64 pairs (half the bytes of one wave per 32 pairs).
@@ -136,7 +136,7 @@ __device__ __forceinline__ void job(const Params &P, int id, unsigned char *lds)
   const int half = wave >> 1; // this wave's half of the key range
   const int h = lane >> 5;
   const int col = lane & 31;
-  // LDS: per key half, two buffers of one K tile (fragment-major) and one V tile (swizzled);
+  // LDS: per key half, two buffers of one K tile and one V tile (both swizzled rows);
   // the two waves of a half (one per pair group) share them.
   uint16_t *sK = reinterpret_cast<uint16_t *>(lds) + half * 2 * kTile;
   uint16_t *sV = reinterpret_cast<uint16_t *>(lds) + (4 + half * 2) * kTile;
@@ -188,31 +188,26 @@ __device__ __forceinline__ void job(const Params &P, int id, unsigned char *lds)
       (void *)(P.k_cache + int64_t(kvh) * kD), 0, int(extent), 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
       (void *)(P.v_cache + int64_t(kvh) * kD), 0, int(extent), 0x00020000);
-  const uint32_t k_lane_off = uint32_t(8 * h) * 2u;
-  const uint32_t v_chunk = uint32_t((lane & 15) ^ (4 * ((lane >> 4) & 3)));
+  // A DMA lands lane i's 16 bytes at slot i % 16 of row i / 16 of its four rows, so lane i reads
+  // the global chunk that belongs there: (i % 16) ^ swz(row).
+  const uint32_t d_chunk = uint32_t((lane & 15) ^ (4 * ((lane >> 4) & 3)));
   // Tile t of this half into buffer t % 2: sixteen DMAs of 1 KiB, the half's wave of pair group
-  // g issuing K fragments 4 g .. + 3 (keys k0 + col, dims 16 f + 8 h .. + 7, in lane order) and
-  // V blocks 4 g .. + 3 (four rows, chunks swizzled); keys past k_hi re-read k_hi - 1.
+  // g issuing row blocks 4 g .. + 3 (rows 4 f .. 4 f + 3 of the tile) of K and of V; keys past
+  // k_hi re-read k_hi - 1.
   auto issue_tile = [&](int t) {
     const int k0 = k_lo + t * kKT;
     const int buf = t & 1;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int f = 4 * grp + i;
-      const uint32_t kkey = uint32_t(min(k0 + col, k_hi - 1));
-      const uint32_t koff = __umul24(kkey, tok_bytes) + uint32_t(16 * f) * 2u + k_lane_off;
+      const uint32_t key = uint32_t(min(k0 + 4 * f + (lane >> 4), k_hi - 1));
+      const uint32_t off = __umul24(key, tok_bytes) + ((d_chunk ^ uint32_t(f & 3)) << 4);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rk, (__attribute__((address_space(3))) void *)(sK + buf * kTile + f * 512), 16,
-          int(koff), 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f = 4 * grp + i;
-      const uint32_t vkey = uint32_t(min(k0 + 4 * f + (lane >> 4), k_hi - 1));
-      const uint32_t voff = __umul24(vkey, tok_bytes) + ((v_chunk ^ uint32_t(f & 3)) << 4);
+          int(off), 0, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rv, (__attribute__((address_space(3))) void *)(sV + buf * kTile + f * 512), 16,
-          int(voff), 0, 0, 0);
+          int(off), 0, 0, 0);
     }
   };
 
@@ -227,6 +222,12 @@ __device__ __forceinline__ void job(const Params &P, int id, unsigned char *lds)
   const int L16 = lane & 15;
   const int tr_row = L16 >> 2;
   const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (L16 & 3);
+  // Byte offsets of this lane's K fragment reads: A[key][dim] of the scores' product, lane
+  // (col, h) holding key col and dims 16 kd + 8 h .. + 7, i.e. chunk 2 kd + h of row col.
+  uint32_t kofs[8];
+#pragma unroll
+  for (int kd = 0; kd < 8; ++kd)
+    kofs[kd] = uint32_t(col * kD * 2 + (((2 * kd + h) ^ swz(col)) << 4));
   uint32_t vofs[8];  // byte offsets of this lane's transpose reads for 16-key step 0
 #pragma unroll
   for (int md = 0; md < 4; ++md) {
@@ -249,17 +250,11 @@ __device__ __forceinline__ void job(const Params &P, int id, unsigned char *lds)
                  : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]), "+v"(qf[4]), "+v"(qf[5]),
                    "+v"(qf[6]), "+v"(qf[7]));
     const int buf = t & 1;
-    const uint32_t ka = lds_addr(sK + buf * kTile + lane * 8);
+    const uint32_t kb = lds_addr(sK + buf * kTile);
     const uint32_t vb = lds_addr(sV + buf * kTile);
     bf16x8 kf[8];
-    ds_read_b128<0 * 1024>(kf[0], ka);
-    ds_read_b128<1 * 1024>(kf[1], ka);
-    ds_read_b128<2 * 1024>(kf[2], ka);
-    ds_read_b128<3 * 1024>(kf[3], ka);
-    ds_read_b128<4 * 1024>(kf[4], ka);
-    ds_read_b128<5 * 1024>(kf[5], ka);
-    ds_read_b128<6 * 1024>(kf[6], ka);
-    ds_read_b128<7 * 1024>(kf[7], ka);
+#pragma unroll
+    for (int kd = 0; kd < 8; ++kd) ds_read_b128<0>(kf[kd], kb + kofs[kd]);
     // S^T (32 keys x 32 pairs): s[4j + i] is key k0 + 8 j + 4 h + i of pair `col`.
     f32x16 s;
 #pragma unroll
