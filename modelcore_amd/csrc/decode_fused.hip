@@ -782,7 +782,29 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
   const int g_first = d.x, nseg = d.y;
   // No keys (a row outside the cache: NaN written), or a unit written directly.
   if (nseg == 0 || (!PRE && nseg == 1)) return;
+  // The slots loaded up front in two passes: their maximum, then each weighted against it (the
+  // weights independent of one another, not a chain of rescales); later segments online.
   float M = -INFINITY, L = 0.f, t0 = 0.f, t1 = 0.f;
+#pragma unroll
+  for (int k = 0; k < SPEC; ++k)
+    if (k < nseg) M = fmaxf(M, ml[k].x);
+  if constexpr (PRE) {
+#pragma unroll
+    for (int k = 0; k < NP; ++k)
+      if (k < P.n_pre) M = fmaxf(M, pml[k].x);
+  }
+  auto weigh = [&](float2 mlk, float2 vk, bool valid) {
+    const float w = valid ? exp2_or_zero(mlk.x - M) : 0.f;
+    L = fmaf(valid ? mlk.y : 0.f, w, L);
+    t0 = fmaf(valid ? vk.x : 0.f, w, t0);
+    t1 = fmaf(valid ? vk.y : 0.f, w, t1);
+  };
+#pragma unroll
+  for (int k = 0; k < SPEC; ++k) weigh(ml[k], v[k], k < nseg);
+  if constexpr (PRE) {
+#pragma unroll
+    for (int k = 0; k < NP; ++k) weigh(pml[k], pv[k], k < P.n_pre);
+  }
   auto add = [&](float2 mlk, float2 vk, bool valid) {
     const float mk = valid ? mlk.x : -INFINITY;
     const float m_new = fmaxf(M, mk);
@@ -792,8 +814,6 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
     t1 = t1 * fa + (valid ? vk.y : 0.f) * fb;
     M = m_new;
   };
-#pragma unroll
-  for (int k = 0; k < SPEC; ++k) add(ml[k], v[k], k < nseg);
   for (int s0 = SPEC; s0 < nseg; s0 += BATCH) {
     float2 mb[BATCH], vb[BATCH];
 #pragma unroll
@@ -804,10 +824,6 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
     }
 #pragma unroll
     for (int k = 0; k < BATCH; ++k) add(mb[k], vb[k], s0 + k < nseg);
-  }
-  if constexpr (PRE) {
-#pragma unroll
-    for (int k = 0; k < NP; ++k) add(pml[k], pv[k], k < P.n_pre);
   }
   const float inv = 1.f / L;
   *reinterpret_cast<uint32_t *>(P.out + (int64_t(b) * P.H + int64_t(kvh) * P.G + hc * GM + hh) * D +
