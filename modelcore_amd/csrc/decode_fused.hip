@@ -123,9 +123,10 @@ struct FusedParams {
   int advance;
   int shared;  // keys [0, shared) are read from row 0 for every row
   // Prefix on the matrix cores: this pass covers keys from lo_floor on, and the merge pass also
-  // folds in n_pre partials per unit (slots unit * n_pre + j of `pre`) made for keys below it.
+  // folds in n_pre partials per unit (slots unit * n_pre + j of `pre`, kPrefixPartBytes each:
+  // bf16 o, fp32 (m, l)) made for keys below it.
   int lo_floor;
-  const float *pre;
+  const char *pre;
   int n_pre;
   int B, H, H_kv, G, n_hc, n_kg, n_units, T_max, window, n_groups;
   int scan32;  // B <= 64 and every sum of row slot counts fits in 31 bits
@@ -766,9 +767,10 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
   if constexpr (PRE) {
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
-      const float *ps = P.pre + (int64_t(ug) * P.n_pre + min(k, P.n_pre - 1)) * kPart;
-      pml[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * hr);
-      pv[k] = *reinterpret_cast<const float2 *>(ps + hr * D + 2 * lane);
+      const char *ps = P.pre + (int64_t(ug) * P.n_pre + min(k, P.n_pre - 1)) * kPrefixPartBytes;
+      pml[k] = *reinterpret_cast<const float2 *>(ps + kPrefixPartOBytes + 8 * hr);
+      const uint32_t o2 = *reinterpret_cast<const uint32_t *>(ps + (hr * D + 2 * lane) * 2);
+      pv[k] = make_float2(__uint_as_float(o2 << 16), __uint_as_float(o2 & 0xffff0000u));
     }
   }
   // The loads above stay ahead of the branch below: the compiler would otherwise sink them past
@@ -869,7 +871,7 @@ size_t decode_prefix_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int
       !prefill_mfma_geometry_ok(n_head, n_kv_head, t_max))
     return 0;
   const int64_t units = batch * decode_fused_units(n_head, n_kv_head);
-  return size_t(units * kPrefixMaxSplits * kPart * 4);
+  return size_t(units * kPrefixMaxSplits * kPrefixPartBytes);
 }
 
 bool decode_fused_supported(const AttnArgs &a) {
@@ -930,7 +932,7 @@ int launch_decode_fused(const AttnArgs &a) {
     P.n_pre = px::splits(a.batch, a.n_head, a.n_kv_head, a.shared_prefix, device_cus(),
                          kPrefixMaxSplits);
     P.lo_floor = int(a.shared_prefix);
-    float *pre = reinterpret_cast<float *>(ws + base_ws);
+    char *pre = ws + base_ws;
     P.pre = pre;
     X.q = static_cast<const uint16_t *>(a.q);
     X.k_cache = static_cast<const uint16_t *>(a.k_cache);

@@ -75,12 +75,16 @@ constexpr int kDecodePartFloats =
 
 // Shared prompt prefix on the matrix cores: for every KV head, the queries of all rows against
 // keys [0, prefix) of row 0, in n_split key ranges; each range's unnormalised (o, m, l) per
-// (row, query head) goes to the fused decode's partial-slot layout, slot (unit * n_split +
-// range), for its merge pass to fold in.
+// (row, query head) goes to slot (unit * n_split + range) of kPrefixPartBytes, for the decode's
+// merge pass to fold in. A slot holds o[kv][q][128] as bf16 (the fp32 sum rounded once), then
+// (m, l)[kv][q] as fp32: half the bytes of an fp32 partial, which the jobs write and the merge
+// reads back once per layer.
 #ifndef MCAMD_PREFIX_SPLITS
 #define MCAMD_PREFIX_SPLITS 16
 #endif
 constexpr int kPrefixMaxSplits = MCAMD_PREFIX_SPLITS;
+constexpr int kPrefixPartOBytes = kDecodeUnitKv * kDecodeUnitQ * 128 * 2;
+constexpr int kPrefixPartBytes = kPrefixPartOBytes + 2 * kDecodeUnitKv * kDecodeUnitQ * 4;
 // Bytes of workspace past decode_workspace_bytes() for those partials (0 where the fused decode
 // never takes the prefix on the matrix cores: such calls read row 0's keys in the streaming pass).
 size_t decode_prefix_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,

@@ -55,10 +55,11 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct Params {
   const uint16_t *q, *k_cache, *v_cache;  // q: (rows, H, D); keys and values of cache row 0
-  float *part;  // slot ((row * n_units + unit) * n_split + range) of kDecodePartFloats floats
+  char *part;  // slot ((row * n_units + unit) * n_split + range) of kPrefixPartBytes
   int H, H_kv, G, n_pairs, n_pb, n_split, key_len, prefix, n_units, n_hc, T_max, jobs;
   float scale_log2;
 };
@@ -381,26 +382,26 @@ __device__ __forceinline__ void job(const Params &P, int id, unsigned char *lds)
   // (row, KV-head group, query-head group), entry (KV head, query head) within it.
   const int unit = (kvh / kDecodeUnitKv) * P.n_hc + head / kDecodeUnitQ;
   const int entry = (kvh % kDecodeUnitKv) * kDecodeUnitQ + head % kDecodeUnitQ;
-  float *slot =
-      P.part + ((int64_t(row) * P.n_units + unit) * P.n_split + split) * kDecodePartFloats;
-  float *po = slot + entry * kD + 4 * h;  // o[md][4 j + i] is dim 32 md + 8 j + 4 h + i
+  char *slot =
+      P.part + ((int64_t(row) * P.n_units + unit) * P.n_split + split) * kPrefixPartBytes;
+  // o[md][4 j + i] is dim 32 md + 8 j + 4 h + i; four of them rounded to bf16 make 8 bytes.
+  uint16_t *po = reinterpret_cast<uint16_t *>(slot) + entry * kD + 4 * h;
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm) {
     const int md = 2 * half + mm;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float a[4];
+      f32x4 a;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int idx = (md * 16 + 4 * j + i) * 64 + lane;
         a[i] = fmaf(f0, r0[idx], f1 * r1[idx]);
       }
-      *reinterpret_cast<float4 *>(po + 32 * md + 8 * j) = make_float4(a[0], a[1], a[2], a[3]);
+      *reinterpret_cast<bf16x4 *>(po + 32 * md + 8 * j) = __builtin_convertvector(a, bf16x4);
     }
   }
   if (half == 0 && h == 0)
-    *reinterpret_cast<float2 *>(slot + kDecodeUnitKv * kDecodeUnitQ * kD + 2 * entry) =
-        make_float2(M, L);
+    *reinterpret_cast<float2 *>(slot + kPrefixPartOBytes + 8 * entry) = make_float2(M, L);
 }
 
 }  // namespace px

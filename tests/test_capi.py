@@ -61,8 +61,9 @@ def test_workspace_size_follows_the_split_count():
     # (H = 16 query heads over 4 KV heads: one unit per row)
     fused = (16 * B + 1024 + B) * (16 * (D + 2)) * 4 + B * 8
     # and, with no window and rows x query heads >= 64, sixteen shared-prefix partial slots per
-    # unit past that (32 rows x 4 query heads per KV head here)
-    prefix = B * 16 * (16 * (D + 2)) * 4
+    # unit past that (32 rows x 4 query heads per KV head here): o of 16 heads in bf16, then
+    # their (m, l) in fp32
+    prefix = B * 16 * (16 * D * 2 + 16 * 2 * 4)
     base = -(-max(general, fused) // 256) * 256
     got = lib.mcamd_attn_workspace_bytes(B, 1, H, 4, D, T_max, -1)
     assert got == base + prefix  # scratch only, no counters
@@ -93,7 +94,7 @@ def test_shared_prefix_slots_only_where_the_matrix_core_kernel_takes_the_geometr
     offsets. Elsewhere the workspace holds no prefix slots and the decode pass reads row 0."""
     lib = _ext.lib()
     D = 128
-    prefix_slots = lambda units: units * 16 * (16 * (D + 2)) * 4  # noqa: E731
+    prefix_slots = lambda units: units * 16 * (16 * D * 2 + 16 * 2 * 4)  # noqa: E731
     # 16 KV heads at 2^16 positions: offsets fit; at 2^20 they do not
     for T_max, takes in ((1 << 16, True), (1 << 20, False)):
         base, units = _base_workspace(64, 32, 16, D, T_max)
