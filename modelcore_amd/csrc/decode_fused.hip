@@ -32,7 +32,9 @@
 //    to bf16 pairs of consecutive tokens; the V rows of the same two tokens are interleaved with
 //    v_perm_b32, so each v_dot2_f32_bf16 adds two tokens' contributions to one output dim.
 //  * Output: a segment that covers its whole unit writes the normalised output; otherwise it
-//    writes (o, m, l) for its 16 heads to the workspace -- segment j of unit u in bucket slot
+//    writes (o, m, l) for its 16 heads to the workspace (o rounded to bf16 once, m and l fp32:
+//    half the bytes of fp32 partials, for ~0.5 us less per microbench call and 1.3% less per
+//    mixed-window step, measured) -- segment j of unit u in bucket slot
 //    u * 16 + j, segments past the sixteenth in an overflow slot (workgroup + unit, distinct per
 //    segment since units advance with the workgroups) -- and the merge pass -- one wave per
 //    (unit, query head), lane l owning dims 2l and 2l + 1 -- combines a unit's segments by
@@ -89,8 +91,11 @@ constexpr int kMergeDims = 128 / 16 / kMergeSplit;  // dims per lane in that mer
 #define MCAMD_DECODE_SEG_COST 64
 #endif
 constexpr int kSegCost = MCAMD_DECODE_SEG_COST;  // key-free lead slots per unit (see unit_span)
-constexpr int kPart = kDecodePartFloats;  // floats per partial: o[16][D], (m, l)[16]
-static_assert(kPart == KG * GM * D + 2 * KG * GM, "partial slot layout");
+// A partial slot: o[16][D] in bf16 (each fp32 sum rounded once, to nearest even), then
+// (m, l)[16] in fp32 -- the same layout as the shared prefix's slots.
+constexpr int kSlot = kPrefixPartBytes;
+constexpr int kSlotO = kPrefixPartOBytes;
+static_assert(kSlotO == KG * GM * D * 2 && kSlot == kSlotO + KG * GM * 8, "partial slot layout");
 #ifndef MCAMD_DECODE_BUCKET
 #define MCAMD_DECODE_BUCKET 16
 #endif
@@ -116,8 +121,8 @@ struct FusedParams {
   uint16_t *k_cache, *v_cache;
   const int32_t *seqlens;
   uint16_t *out;
-  float *part;  // [B * n_units * kBucket][kPart]: segment j < kBucket of unit u at u * kBucket + j
-  float *over;  // [kMaxGroups + B * n_units][kPart]: segments j >= kBucket, slot = group + unit
+  char *part;  // [B * n_units * kBucket] slots: segment j < kBucket of unit u at u * kBucket + j
+  char *over;  // [kMaxGroups + B * n_units] slots: segments j >= kBucket, slot = group + unit
   int2 *desc;   // [B * n_units]: (first workgroup, segments) of each unit; (0, 0): no keys
   int32_t *adv_seqlens;  // the merge pass adds `advance` to every row's position (0: it does not)
   int advance;
@@ -664,14 +669,18 @@ __device__ __forceinline__ void decode_fused_body(
       // workgroup is at least this unit's last). The merge kernel, launched next on the same
       // stream, combines a unit's partials.
       const int j = g - g_first;
-      float *slot = j < kBucket ? P.part + (int64_t(ug) * kBucket + j) * kPart
-                                : P.over + int64_t(g + ug) * kPart;
-      float *po = slot + (mr * GM + mh) * D + d0;
+      char *slot = j < kBucket ? P.part + (int64_t(ug) * kBucket + j) * kSlot
+                               : P.over + int64_t(g + ug) * kSlot;
+      uint32_t w[kMergeDims / 2];
 #pragma unroll
-      for (int e4 = 0; e4 < kMergeDims; e4 += 4)
-        *reinterpret_cast<float4 *>(po + e4) = make_float4(acc[e4], acc[e4 + 1], acc[e4 + 2], acc[e4 + 3]);
+      for (int e = 0; e < kMergeDims / 2; ++e) w[e] = pack_bf16(acc[2 * e], acc[2 * e + 1]);
+      char *po = slot + ((mr * GM + mh) * D + d0) * 2;
+      if constexpr (kMergeDims == 8)
+        *reinterpret_cast<uint4 *>(po) = make_uint4(w[0], w[1], w[2], w[3]);
+      else
+        *reinterpret_cast<uint2 *>(po) = make_uint2(w[0], w[1]);
       if (c == 0 && wv < KG)
-        *reinterpret_cast<float2 *>(slot + KG * GM * D + 2 * (mr * GM + mh)) = make_float2(M, L);
+        *reinterpret_cast<float2 *>(slot + kSlotO + 8 * (mr * GM + mh)) = make_float2(M, L);
     }
     lds_barrier();  // s_acc is reused by the next segment
 
@@ -721,10 +730,10 @@ decode_fused_prefix_kernel(const int32_t *a_seqlens, const uint16_t *a_q, uint16
 // passed separately so that they arrive preloaded in SGPRs.
 template <int SPEC, int NP>
 __global__ __launch_bounds__(64) void decode_merge_kernel(
-    const float *__restrict__ a_part, const int2 *__restrict__ a_desc, uint16_t *a_out,
+    const char *__restrict__ a_part, const int2 *__restrict__ a_desc, uint16_t *a_out,
     int32_t *a_adv, int a_n_units, int a_n_hc, int a_H_kv, int a_G, int a_H, int a_advance,
     FusedParams P) {
-  P.part = const_cast<float *>(a_part);
+  P.part = const_cast<char *>(a_part);
   P.desc = const_cast<int2 *>(a_desc);
   P.out = a_out;
   P.adv_seqlens = a_adv;
@@ -748,9 +757,17 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
   // before its own loads (one wave and lane per row adds, so it is a plain increment).
   if (P.advance != 0 && unit == 0 && hr == 0 && lane == 0) atomicAdd(P.adv_seqlens + b, P.advance);
   if (kvh >= P.H_kv || hh >= min(GM, P.G - hc * GM)) return;
-  const float *bucket = P.part + int64_t(ug) * kBucket * kPart;
-  auto seg_at = [&](int j, int g_first) {
-    return j < kBucket ? bucket + int64_t(j) * kPart : P.over + int64_t(g_first + j + ug) * kPart;
+  const char *bucket = P.part + int64_t(ug) * kBucket * kSlot;
+  auto seg_at = [&](int j, int g_first) -> const char * {
+    return j < kBucket ? bucket + int64_t(j) * kSlot : P.over + int64_t(g_first + j + ug) * kSlot;
+  };
+  // (m, l) and this lane's two dims of o (bf16) of head hr in a slot.
+  auto slot_ml = [&](const char *ps) {
+    return *reinterpret_cast<const float2 *>(ps + kSlotO + 8 * hr);
+  };
+  auto slot_v = [&](const char *ps) {
+    const uint32_t o2 = *reinterpret_cast<const uint32_t *>(ps + (hr * D + 2 * lane) * 2);
+    return make_float2(__uint_as_float(o2 << 16), __uint_as_float(o2 & 0xffff0000u));
   };
   // The unit's (first workgroup, segments), published by the streaming pass: no segments for a
   // row outside the cache (its NaN output is written), one for a unit written directly.
@@ -758,19 +775,18 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
   float2 ml[SPEC], v[SPEC];
 #pragma unroll
   for (int k = 0; k < SPEC; ++k) {
-    const float *ps = bucket + int64_t(k) * kPart;
-    ml[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * hr);
-    v[k] = *reinterpret_cast<const float2 *>(ps + hr * D + 2 * lane);
+    const char *ps = bucket + int64_t(k) * kSlot;
+    ml[k] = slot_ml(ps);
+    v[k] = slot_v(ps);
   }
   constexpr bool PRE = NP > 0;
   float2 pml[PRE ? NP : 1], pv[PRE ? NP : 1];
   if constexpr (PRE) {
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
-      const char *ps = P.pre + (int64_t(ug) * P.n_pre + min(k, P.n_pre - 1)) * kPrefixPartBytes;
-      pml[k] = *reinterpret_cast<const float2 *>(ps + kPrefixPartOBytes + 8 * hr);
-      const uint32_t o2 = *reinterpret_cast<const uint32_t *>(ps + (hr * D + 2 * lane) * 2);
-      pv[k] = make_float2(__uint_as_float(o2 << 16), __uint_as_float(o2 & 0xffff0000u));
+      const char *ps = P.pre + (int64_t(ug) * P.n_pre + min(k, P.n_pre - 1)) * kSlot;
+      pml[k] = slot_ml(ps);
+      pv[k] = slot_v(ps);
     }
   }
   // The loads above stay ahead of the branch below: the compiler would otherwise sink them past
@@ -820,9 +836,9 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
     float2 mb[BATCH], vb[BATCH];
 #pragma unroll
     for (int k = 0; k < BATCH; ++k) {
-      const float *ps = seg_at(min(s0 + k, nseg - 1), g_first);
-      mb[k] = *reinterpret_cast<const float2 *>(ps + KG * GM * D + 2 * hr);
-      vb[k] = *reinterpret_cast<const float2 *>(ps + hr * D + 2 * lane);
+      const char *ps = seg_at(min(s0 + k, nseg - 1), g_first);
+      mb[k] = slot_ml(ps);
+      vb[k] = slot_v(ps);
     }
 #pragma unroll
     for (int k = 0; k < BATCH; ++k) add(mb[k], vb[k], s0 + k < nseg);
@@ -859,7 +875,7 @@ size_t decode_fused_partial_bytes(int64_t batch, int64_t n_head, int64_t n_kv_he
   (void)t_max;
   (void)window;
   const int64_t units = batch * decode_fused_units(n_head, n_kv_head);
-  return size_t((units * kBucket + kMaxGroups + units) * kPart * 4 + units * int64_t(sizeof(int2)));
+  return size_t((units * kBucket + kMaxGroups + units) * kSlot + units * int64_t(sizeof(int2)));
 }
 
 size_t decode_prefix_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,
@@ -871,7 +887,7 @@ size_t decode_prefix_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int
       !prefill_mfma_geometry_ok(n_head, n_kv_head, t_max))
     return 0;
   const int64_t units = batch * decode_fused_units(n_head, n_kv_head);
-  return size_t(units * kPrefixMaxSplits * kPrefixPartBytes);
+  return size_t(units * kPrefixMaxSplits * kSlot);
 }
 
 bool decode_fused_supported(const AttnArgs &a) {
@@ -914,9 +930,9 @@ int launch_decode_fused(const AttnArgs &a) {
   P.n_groups = int(groups);
   char *ws = static_cast<char *>(a.workspace);
   const int64_t units = int64_t(P.B) * P.n_units;
-  P.part = reinterpret_cast<float *>(ws);
-  P.over = P.part + units * kBucket * kPart;
-  P.desc = reinterpret_cast<int2 *>(P.over + (kMaxGroups + units) * kPart);
+  P.part = ws;
+  P.over = P.part + units * kBucket * kSlot;
+  P.desc = reinterpret_cast<int2 *>(P.over + (kMaxGroups + units) * kSlot);
   // A long shared prompt prefix of a wide batch goes to the matrix cores (every row's queries
   // against row 0's prefix keys at once, in key ranges) when the workspace has room for those
   // partials; this pass then covers each row's own keys only, and the merge folds both.

@@ -67,18 +67,18 @@ size_t decode_workspace_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, 
                               int64_t t_max, int64_t window);
 
 // Units of the fused decode: one row's group of kDecodeUnitKv KV heads and kDecodeUnitQ query
-// heads of each. A partial slot holds o[kv][q][128] then (m, l)[kv][q], fp32.
+// heads of each. A unit's split partials use the slot layout of kPrefixPartBytes below.
 constexpr int kDecodeUnitKv = 4;
 constexpr int kDecodeUnitQ = 4;
-constexpr int kDecodePartFloats =
-    kDecodeUnitKv * kDecodeUnitQ * 128 + 2 * kDecodeUnitKv * kDecodeUnitQ;
 
+// A split partial of a decode unit (the fused decode's segments and the shared prompt's key
+// ranges): o[kv][q][128] as bf16 (each fp32 sum rounded once, to nearest even), then
+// (m, l)[kv][q] as fp32 -- half the bytes of an all-fp32 slot, written by one launch and read
+// back by the merge pass.
 // Shared prompt prefix on the matrix cores: for every KV head, the queries of all rows against
 // keys [0, prefix) of row 0, in n_split key ranges; each range's unnormalised (o, m, l) per
-// (row, query head) goes to slot (unit * n_split + range) of kPrefixPartBytes, for the decode's
-// merge pass to fold in. A slot holds o[kv][q][128] as bf16 (the fp32 sum rounded once), then
-// (m, l)[kv][q] as fp32: half the bytes of an fp32 partial, which the jobs write and the merge
-// reads back once per layer.
+// (row, query head) goes to slot (unit * n_split + range), for the decode's merge pass to fold
+// in.
 #ifndef MCAMD_PREFIX_SPLITS
 #define MCAMD_PREFIX_SPLITS 16
 #endif

@@ -56,20 +56,21 @@ def test_workspace_size_follows_the_split_count():
     B, H, D, T_max = 32, 16, 128, 8300
     n_splits = -(-T_max // 256)
     general = B * H * n_splits * (D + 2) * 4  # per-(row, head, split) partials, general kernel
-    # per-segment partials (16 heads), bf16 / D=128: a bucket of 16 slots per unit, an overflow
-    # area of 1024 + units slots, then one (first group, segments) int pair per unit
-    # (H = 16 query heads over 4 KV heads: one unit per row)
-    fused = (16 * B + 1024 + B) * (16 * (D + 2)) * 4 + B * 8
+    # per-segment partials (16 heads: o in bf16, (m, l) in fp32), bf16 / D=128: a bucket of 16
+    # slots per unit, an overflow area of 1024 + units slots, then one (first group, segments)
+    # int pair per unit (H = 16 query heads over 4 KV heads: one unit per row)
+    slot = 16 * D * 2 + 16 * 2 * 4
+    fused = (16 * B + 1024 + B) * slot + B * 8
     # and, with no window and rows x query heads >= 64, sixteen shared-prefix partial slots per
     # unit past that (32 rows x 4 query heads per KV head here): o of 16 heads in bf16, then
     # their (m, l) in fp32
-    prefix = B * 16 * (16 * D * 2 + 16 * 2 * 4)
+    prefix = B * 16 * slot
     base = -(-max(general, fused) // 256) * 256
     got = lib.mcamd_attn_workspace_bytes(B, 1, H, 4, D, T_max, -1)
     assert got == base + prefix  # scratch only, no counters
     # 8 rows x 4 query heads per KV head: too few for the matrix cores, no prefix slots
     general8 = 8 * H * n_splits * (D + 2) * 4
-    fused8 = (16 * 8 + 1024 + 8) * (16 * (D + 2)) * 4 + 8 * 8
+    fused8 = (16 * 8 + 1024 + 8) * slot + 8 * 8
     assert lib.mcamd_attn_workspace_bytes(8, 1, H, 4, D, T_max, -1) == \
         -(-max(general8, fused8) // 256) * 256
     windowed = lib.mcamd_attn_workspace_bytes(B, 1, H, 4, D, T_max, 1024)
@@ -84,7 +85,7 @@ def _base_workspace(B, H, H_kv, D, T_max, window=-1):
     n_splits = -(-(T_max if window < 0 else min(T_max, window + 1)) // 256)
     general = B * H * n_splits * (D + 2) * 4
     units = B * -(-H_kv // 4) * -(-(H // H_kv) // 4)
-    fused = (16 * units + 1024 + units) * (16 * (D + 2)) * 4 + units * 8
+    fused = (16 * units + 1024 + units) * (16 * D * 2 + 16 * 2 * 4) + units * 8
     return -(-max(general, fused) // 256) * 256, units
 
 

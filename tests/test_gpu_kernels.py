@@ -385,6 +385,7 @@ def test_decode_at_batch_32_gqa_16_4_hd128_context_8k():
         kb[0, L], vb[0, L] = to_np(k)[b, 0], to_np(v)[b, 0]
         ref = ko.attention(to_np(q)[b:b + 1], kb, vb, [L], -1)
         worst = max(worst, max_abs(out[b:b + 1], ref))
+    print(f"max-abs against the float64 oracle {worst:.2e}", flush=True)
     assert worst <= ATOL[torch.bfloat16], f"max-abs {worst}"
     got = gg["k_cache"]
     for b in range(B):
