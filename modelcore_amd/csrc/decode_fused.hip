@@ -93,8 +93,8 @@ constexpr int kMergeDims = 128 / 16 / kMergeSplit;  // dims per lane in that mer
 constexpr int kSegCost = MCAMD_DECODE_SEG_COST;  // key-free lead slots per unit (see unit_span)
 // A partial slot: o[16][D] in bf16 (each fp32 sum rounded once, to nearest even), then
 // (m, l)[16] in fp32 -- the same layout as the shared prefix's slots.
-constexpr int kSlot = kPrefixPartBytes;
-constexpr int kSlotO = kPrefixPartOBytes;
+constexpr int kSlot = kPartSlotBytes;
+constexpr int kSlotO = kPartSlotOBytes;
 static_assert(kSlotO == KG * GM * D * 2 && kSlot == kSlotO + KG * GM * 8, "partial slot layout");
 #ifndef MCAMD_DECODE_BUCKET
 #define MCAMD_DECODE_BUCKET 16
@@ -128,7 +128,7 @@ struct FusedParams {
   int advance;
   int shared;  // keys [0, shared) are read from row 0 for every row
   // Prefix on the matrix cores: this pass covers keys from lo_floor on, and the merge pass also
-  // folds in n_pre partials per unit (slots unit * n_pre + j of `pre`, kPrefixPartBytes each:
+  // folds in n_pre partials per unit (slots unit * n_pre + j of `pre`, kPartSlotBytes each:
   // bf16 o, fp32 (m, l)) made for keys below it.
   int lo_floor;
   const char *pre;

@@ -67,7 +67,7 @@ size_t decode_workspace_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, 
                               int64_t t_max, int64_t window);
 
 // Units of the fused decode: one row's group of kDecodeUnitKv KV heads and kDecodeUnitQ query
-// heads of each. A unit's split partials use the slot layout of kPrefixPartBytes below.
+// heads of each. A unit's split partials use the slot layout of kPartSlotBytes below.
 constexpr int kDecodeUnitKv = 4;
 constexpr int kDecodeUnitQ = 4;
 
@@ -75,6 +75,9 @@ constexpr int kDecodeUnitQ = 4;
 // ranges): o[kv][q][128] as bf16 (each fp32 sum rounded once, to nearest even), then
 // (m, l)[kv][q] as fp32 -- half the bytes of an all-fp32 slot, written by one launch and read
 // back by the merge pass.
+constexpr int kPartSlotOBytes = kDecodeUnitKv * kDecodeUnitQ * 128 * 2;
+constexpr int kPartSlotBytes = kPartSlotOBytes + 2 * kDecodeUnitKv * kDecodeUnitQ * 4;
+
 // Shared prompt prefix on the matrix cores: for every KV head, the queries of all rows against
 // keys [0, prefix) of row 0, in n_split key ranges; each range's unnormalised (o, m, l) per
 // (row, query head) goes to slot (unit * n_split + range), for the decode's merge pass to fold
@@ -83,8 +86,6 @@ constexpr int kDecodeUnitQ = 4;
 #define MCAMD_PREFIX_SPLITS 16
 #endif
 constexpr int kPrefixMaxSplits = MCAMD_PREFIX_SPLITS;
-constexpr int kPrefixPartOBytes = kDecodeUnitKv * kDecodeUnitQ * 128 * 2;
-constexpr int kPrefixPartBytes = kPrefixPartOBytes + 2 * kDecodeUnitKv * kDecodeUnitQ * 4;
 // Bytes of workspace past decode_workspace_bytes() for those partials (0 where the fused decode
 // never takes the prefix on the matrix cores: such calls read row 0's keys in the streaming pass).
 size_t decode_prefix_bytes(int64_t batch, int64_t n_head, int64_t n_kv_head, int64_t head_dim,

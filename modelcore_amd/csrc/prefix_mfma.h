@@ -59,7 +59,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct Params {
   const uint16_t *q, *k_cache, *v_cache;  // q: (rows, H, D); keys and values of cache row 0
-  char *part;  // slot ((row * n_units + unit) * n_split + range) of kPrefixPartBytes
+  char *part;  // slot ((row * n_units + unit) * n_split + range) of kPartSlotBytes
   int H, H_kv, G, n_pairs, n_pb, n_split, key_len, prefix, n_units, n_hc, T_max, jobs;
   float scale_log2;
 };
@@ -383,7 +383,7 @@ __device__ __forceinline__ void job(const Params &P, int id, unsigned char *lds)
   const int unit = (kvh / kDecodeUnitKv) * P.n_hc + head / kDecodeUnitQ;
   const int entry = (kvh % kDecodeUnitKv) * kDecodeUnitQ + head % kDecodeUnitQ;
   char *slot =
-      P.part + ((int64_t(row) * P.n_units + unit) * P.n_split + split) * kPrefixPartBytes;
+      P.part + ((int64_t(row) * P.n_units + unit) * P.n_split + split) * kPartSlotBytes;
   // o[md][4 j + i] is dim 32 md + 8 j + 4 h + i; four of them rounded to bf16 make 8 bytes.
   uint16_t *po = reinterpret_cast<uint16_t *>(slot) + entry * kD + 4 * h;
 #pragma unroll
@@ -401,7 +401,7 @@ __device__ __forceinline__ void job(const Params &P, int id, unsigned char *lds)
     }
   }
   if (half == 0 && h == 0)
-    *reinterpret_cast<float2 *>(slot + kPrefixPartOBytes + 8 * entry) = make_float2(M, L);
+    *reinterpret_cast<float2 *>(slot + kPartSlotOBytes + 8 * entry) = make_float2(M, L);
 }
 
 }  // namespace px
