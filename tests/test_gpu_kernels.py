@@ -387,6 +387,9 @@ def test_decode_at_batch_32_gqa_16_4_hd128_context_8k():
         worst = max(worst, max_abs(out[b:b + 1], ref))
     print(f"max-abs against the float64 oracle {worst:.2e}", flush=True)
     assert worst <= ATOL[torch.bfloat16], f"max-abs {worst}"
+    # Accuracy guard, far inside the tolerance: the outputs are deterministic, and with the split
+    # partials' o rounded to bf16 once this shape measures 9.8e-4 (6.4e-4 with fp32 partials).
+    assert worst <= 2e-3, f"max-abs {worst}: accuracy below what this path delivers"
     got = gg["k_cache"]
     for b in range(B):
         assert torch.equal(got[b, int(seqlens[b])].cpu(), k[b, 0])

@@ -109,6 +109,8 @@ def test_shared_prefix_on_the_matrix_cores_matches_the_oracle(dtype, P, seqlens,
     print(f"max-abs against the unshared call {near:.2e}, against the oracle {err:.2e}",
           flush=True)
     assert err <= ATOL[torch.bfloat16], f"against the oracle: max-abs {err}"
+    # Accuracy guard (deterministic outputs): 4.0e-4 to 1.8e-3 measured on these cases.
+    assert err <= 3e-3, f"against the oracle: max-abs {err}, below what this path delivers"
 
 
 def test_shared_prefix_keys_come_from_row_0():
