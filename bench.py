@@ -846,6 +846,30 @@ def cpu_sample_baseline(budget_s=20.0):
                       f"({t_layer * 1e3:.1f} ms per layer) + {t_head * 1e3:.1f} ms head"}
 
 
+def sample_weight_bytes():
+    """Bytes of the bf16 weights a sampling decode step reads: per layer the stacked QKV
+    (6144 x 4096), c_proj (4096 x 4096), the gate/up stack and down_proj (3 x 14336 x 4096), then
+    the lm_head (32768 x 4096)."""
+    qkv = (SM_H + 2 * SM_HKV) * D * SM_D
+    per_layer = qkv + SM_D * SM_D + 3 * SM_HID * SM_D
+    return 2 * (SM_LAYERS * per_layer + SM_V * SM_D)
+
+
+def sample_step_bytes(first, steps, shared=SM_PROMPT):
+    """Mean bytes a sampling decode step must read at least, over `steps` steps from decode step
+    `first`: the weights, and per layer with the prompt shared (shared > 0) its K/V once plus each
+    row's own keys past it, else every row's K/V (the reference's byte model)."""
+    from modelcore_amd import stats
+    if shared:
+        kv = (sum(stats.decode_step_bytes([SM_PROMPT + first + i - shared] * SM_ROWS, SM_H,
+                                          SM_HKV, D, 2) for i in range(steps)) / steps
+              + 2 * shared * SM_HKV * D * 2) * SM_LAYERS
+    else:
+        kv = sum(stats.decode_step_bytes([SM_PROMPT + first + i] * SM_ROWS, SM_H, SM_HKV, D, 2)
+                 for i in range(steps)) / steps * SM_LAYERS
+    return sample_weight_bytes() + kv
+
+
 def bench_sample(args):
     """Large-batch sampling end to end: a 32-layer model (d_model 4096, 32 q / 8 kv heads of 128,
     gated SiLU MLP 14336, vocab 32768, softcap 15, bf16, random init with seed 0) prefills one
@@ -920,6 +944,8 @@ def bench_sample(args):
         stats.decode_step_bytes([SM_PROMPT + W + i - shared] * SM_ROWS, SM_H, SM_HKV, D, 2)
         for i in range(K)) / K + 2 * shared * SM_HKV * D * 2) * SM_LAYERS
     step_bytes = weight_bytes + kv_hbm
+    assert abs(step_bytes - sample_step_bytes(W, K, shared)) < 1.0, \
+        "the model's cached weight copies differ from the closed-form byte count"
     gbps = step_bytes / (ms * 1e-3) / 1e9
     hbm_peak, _, peak_src = peaks()
     result = {
@@ -943,6 +969,9 @@ def bench_sample(args):
                                "layers + sampling)", "bound": "hbm", "achieved": round(gbps, 1),
                      "peak": hbm_peak / 1e9, "peak_source": peak_src, "unit": "GB/s",
                      "frac": round(gbps * 1e9 / hbm_peak, 4), "traffic": None,
+                     "traffic_source": "not measured: rocprofv3 --pmc stops with a host "
+                                       "segmentation fault at the first launch of "
+                                       "decode_fused_prefix_kernel in this workload",
                      "bytes_per_step": int(step_bytes), "weight_bytes": int(weight_bytes),
                      "kv_bytes_per_step": int(kv_hbm),
                      "kv_note": "with shared_prefix > 0 the prompt's K/V count once per layer "

@@ -88,3 +88,22 @@ def test_summarize_pmc_takes_the_last_dispatches(tmp_path, capsys):
              Counter_Value=v) for d, v in ((1, 1000), (2, 10), (3, 30))])
     bench.summarize_pmc([str(tmp_path / "p.csv")], "prefill_mfma_kernel", 2)
     assert "| SQ_WAVES | 20 |" in capsys.readouterr().out
+
+
+def test_sample_step_bytes_counts_weights_and_the_shared_prompt_once():
+    # bf16 weights: 32 layers of QKV stack (6144 x 4096), c_proj (4096 x 4096), gate/up and
+    # down_proj (3 x 14336 x 4096) = 32 x 218 103 808 elements, plus the 32768 x 4096 lm_head.
+    assert bench.sample_weight_bytes() == 2 * (32 * 218_103_808 + 32768 * 4096) == 14_227_079_168
+    # One decode step at decode step `first`: each row's own keys past the prompt (the new
+    # token's K/V counted as read and written), q and out, plus the prompt's K/V once per layer.
+    first, P = 7, bench.SM_PROMPT
+    own = stats.decode_step_bytes([P + first - P] * bench.SM_ROWS, bench.SM_H, bench.SM_HKV,
+                                  bench.D, 2)
+    prompt = 2 * P * bench.SM_HKV * bench.D * 2
+    assert bench.sample_step_bytes(first, 1) == bench.sample_weight_bytes() + \
+        (own + prompt) * bench.SM_LAYERS
+    # Without the shared prompt: every row's K/V (the reference's byte model).
+    every = stats.decode_step_bytes([P + first] * bench.SM_ROWS, bench.SM_H, bench.SM_HKV,
+                                    bench.D, 2)
+    assert bench.sample_step_bytes(first, 1, shared=0) == bench.sample_weight_bytes() + \
+        every * bench.SM_LAYERS
