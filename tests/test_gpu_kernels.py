@@ -324,7 +324,11 @@ def test_chunked_prefill_of_a_long_prompt_at_gqa_32_8():
     c = make_case([1536], 512, 32, 8, 128, 2048, torch.bfloat16, seed=33)
     out, g = _run_op(c, -1)
     err = max_abs(to_np(out), _oracle(c, -1))
+    print(f"max-abs against the float64 oracle {err:.2e}", flush=True)
     assert err <= ATOL[torch.bfloat16], f"max-abs {err}"
+    # Accuracy guard, far inside the tolerance (deterministic output): 1.7e-3 measured with the
+    # query scale rounded into the bf16 fragments, 1.3e-3 with it applied in fp32.
+    assert err <= 5e-3, f"max-abs {err}: accuracy below what this path delivers"
 
 
 def test_chunked_prefill_through_the_cache_equals_one_full_prefill():
