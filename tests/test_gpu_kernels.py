@@ -297,6 +297,8 @@ PREFILL_CASES = [
     ([250], 300, 8, 8, 128, 600, 63),             # MHA, window inside a tile
     ([5, 400], 40, 16, 2, 128, 448, 64),          # G = 8
     ([1000], 64, 16, 1, 128, 1100, -1),           # G = 16: 16 positions per workgroup
+    ([8000, 6913], 64, 32, 2, 128, 8100, -1),     # G = 16 over long prefixes (126 key tiles)
+    ([7000, 100], 96, 24, 2, 128, 7200, 1500),    # G = 12, a window of 1500 in a long cache
     ([7, 0], 1, 32, 8, 128, 16, -1),              # a single query through the prefill path
     ([17, 3], 25, 16, 4, 80, 64, -1),             # head dims that are not powers of two
     ([100, 0, 31], 70, 12, 4, 96, 200, 50),
