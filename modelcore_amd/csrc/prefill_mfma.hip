@@ -366,7 +366,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(MfmaParams P)
         __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
       else
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-      __syncthreads();
+      // A bare barrier: __syncthreads' fence would make every wave wait for all its DMAs in
+      // flight, the next tile's included, so that tile would have to land a pair of slots early.
+      // Each wave's own vmcnt wait above has put its part of this tile in LDS, and every LDS
+      // read of the buffer the next DMAs overwrite has been consumed before its wave got here.
+      __builtin_amdgcn_s_barrier();
     }
     // Even slots fetch tile slot / 2 + 2 into buffer (slot / 2 + 2) % 4, whose previous tile was
     // last read in slot - 1; the four parts are spread over the slot's work.
